@@ -1,0 +1,239 @@
+"""Benchmark of the MI355X attention hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra]
+
+Headline (one JSON line on stdout): causal GQA prefill attention, B=4, S=2048,
+32 q / 8 kv heads, head_dim 64, fp16, inputs N(0,1)/8 (seed 1), in TFLOP/s of
+algorithmic work (4 B Hq D S(S+1)/2 FLOP per step). A step is one
+``engine.attention.flash_attention`` call on inputs already resident in HBM.
+
+The same line carries
+  roofline      the prefill kernel's achieved TFLOP/s (algorithmic FLOP per
+                launch / average launch duration from HIP events on the launch
+                stream) against the dense fp16 MFMA peak;
+  cpu_baseline  the fp32 oracle (the reference's naive algorithm) timed on the
+                host cores on the same workload;
+  extra         the other workloads: paged decode (B=32, fp16) and speculative
+                verify (B=8, Lq=5, bf16) in GB/s against the 8 TB/s HBM peak,
+                timed while rotating over >= 512 MiB of KV pool copies so the
+                256 MiB Infinity Cache cannot hold them, and the S=16384
+                D=128 bf16 prefill in TFLOP/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "custom-inference-engine_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_MFMA_F16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense fp16/bf16
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    return ap.parse_args()
+
+
+class FlashLaunch:
+    """Pre-bound cie_flash_fwd call (no per-call Python allocation)."""
+
+    def __init__(self, case, dev):
+        import torch
+        from engine import _lib
+
+        self.lib = _lib.load()
+        self.q, self.k, self.v = case.q.to(dev), case.k.to(dev), case.v.to(dev)
+        self.o = torch.empty_like(self.q)
+        B, H, M, D = self.q.shape
+        Hk, N = self.k.shape[1], self.k.shape[2]
+        self._keep = [_lib.strides(t) for t in (self.q, self.k, self.v, self.o)]
+        self.args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(),
+                     *self._keep, B, H, Hk, M, N, D, ctypes.c_float(1.0 / math.sqrt(D)), 1,
+                     _lib.DTYPE_CODES[self.q.dtype], _lib.stream_handle(self.q.device))
+        self.flops = case.flops
+
+    def __call__(self, i=0):
+        rc = self.lib.cie_flash_fwd(*self.args)
+        if rc:
+            from engine import _lib
+            _lib.check(rc)
+
+
+class PagedLaunch:
+    """Pre-bound cie_paged_fwd call rotating over `copies` KV pool copies."""
+
+    def __init__(self, case, dev, min_bytes=512 << 20):
+        import torch
+        from engine import _lib
+
+        self.lib = _lib.load()
+        self.q = case.q.to(dev)
+        pool_bytes = 2 * case.k_pool.numel() * case.k_pool.element_size()
+        self.copies = max(1, -(-min_bytes // pool_bytes))
+        self.pools = [(case.k_pool.to(dev), case.v_pool.to(dev)) for _ in range(self.copies)]
+        self.bt = case.block_tables.to(dev).contiguous()
+        self.lens = case.context_lens.to(dev)
+        self.o = torch.empty_like(self.q)
+        B, Hq, Lq, D = self.q.shape
+        nb, bs, Hk, _ = case.k_pool.shape
+        mb = self.bt.shape[1]
+        mc = int(case.context_lens.max())
+        ws = self.lib.cie_paged_workspace_bytes(B, Hq, Hk, Lq, D, mc, bs, mb)
+        self.ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self._keep = [_lib.strides(t) for t in (self.q, self.pools[0][0], self.pools[0][1], self.o)]
+        self.head = (self.q.data_ptr(),)
+        self.tail = (self.bt.data_ptr(), self.lens.data_ptr(), self.o.data_ptr(), self.ws.data_ptr(), ws,
+                     *self._keep, B, Hq, Hk, Lq, D, nb, bs, mb, mc, ctypes.c_float(1.0 / math.sqrt(D)), 1,
+                     _lib.DTYPE_CODES[self.q.dtype], _lib.stream_handle(self.q.device))
+        self.ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in self.pools]
+        self.bytes = case.bytes
+        self.flops = case.flops
+
+    def __call__(self, i=0):
+        kp, vp = self.ptrs[i % self.copies]
+        rc = self.lib.cie_paged_fwd(self.q.data_ptr(), kp, vp, *self.tail)
+        if rc:
+            from engine import _lib
+            _lib.check(rc)
+
+
+def event_time_ms(fn, n, warmup, trials=3):
+    """Median over trials of (HIP-event time of n back-to-back launches) / n."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    res = []
+    for _ in range(trials):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(n):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        res.append(a.elapsed_time(b) / n)
+    return statistics.median(res)
+
+
+def cpu_baseline(case):
+    """The reference's algorithm (fp32 up-cast, repeat_interleave GQA, full
+    score matrix, bottom-right mask, softmax, PV) on the host cores."""
+    import torch
+    from oracle import flash_attention_ref
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    q, k, v = case.q.float(), case.k.float(), case.v.float()
+    flash_attention_ref(q[:1, :8], k[:1, :2], v[:1, :2], causal=True)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        flash_attention_ref(q, k, v, causal=True)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(case.flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"full {case.name} workload through the fp32 oracle (unchunked: 4x32x2048x2048 "
+                      f"score matrix), median of 3 runs, {t:.2f} s each"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    from benchmarks import workloads
+    from engine.attention import flash_attention
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    case = workloads.prefill_s2048()
+    q, k, v = case.q.to(dev), case.k.to(dev), case.v.to(dev)
+
+    # headline: K steps of the public entry point
+    for _ in range(args.warmup):
+        flash_attention(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        flash_attention(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    value = case.flops / (ms_per_step / 1e3) / 1e12
+
+    # roofline of the prefill kernel: event-timed back-to-back launches
+    fl = FlashLaunch(case, dev)
+    kern_ms = event_time_ms(fl, max(20, args.steps), 3)
+    achieved = case.flops / (kern_ms / 1e3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
+            "kernel": "flash_fwd_kernel<fp16, D=64>", "kernel_us": round(kern_ms * 1e3, 2)}
+
+    extra = {}
+    if not args.no_extra:
+        for name in ("decode_b32", "verify_b8"):
+            c = workloads.WORKLOADS[name]()
+            pl = PagedLaunch(c, dev)
+            ms = event_time_ms(pl, 40 * pl.copies, 2 * pl.copies)
+            gbs = c.bytes / (ms / 1e3) / 1e9
+            extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
+                           "bytes": int(c.bytes), "pool_copies": pl.copies,
+                           "dtype": "fp16" if c.q.dtype == torch.float16 else "bf16"}
+            del pl
+        c5 = workloads.prefill_s16384()
+        f5 = FlashLaunch(c5, dev)
+        ms = event_time_ms(f5, 5, 1)
+        t5 = c5.flops / (ms / 1e3) / 1e12
+        extra["prefill_s16384"] = {"TFLOP/s": round(t5, 2), "frac_mfma": round(t5 / PEAK_MFMA_F16_TFLOPS, 4),
+                                   "us": round(ms * 1e3, 1), "dtype": "bf16"}
+        del f5
+        torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(case)
+
+    line = {
+        "metric": "prefill attention TFLOP/s + paged-decode KV GB/s (% roofline) on 1 MI355X",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "prefill_s2048", "B": 4, "S": 2048, "Hq": 32, "Hk": 8, "head_dim": 64,
+                   "causal": True, "flop_per_step": case.flops},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

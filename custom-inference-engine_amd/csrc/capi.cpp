@@ -1,0 +1,220 @@
+// C ABI of libcie_attn.so: argument validation, error reporting and launch.
+//
+// Validation mirrors the checks the reference performs before it launches
+// (engine/attention.py:17-25, kernels/flash_attention.py:147-165) and turns
+// them into status codes; the Python layer maps the codes back onto the
+// reference's exception types.
+#include <cmath>
+#include <cstdio>
+#include <cstdarg>
+#include <string>
+
+#include "cie_attn.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+bool head_dim_ok(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// head_dim stride 1, outer strides non-negative and 16-byte multiples (the
+// kernels move rows in 16-byte vectors).
+int check_strides(const char* name, const int64_t* st) {
+  if (!st) return fail(CIE_EINVAL, "%s: stride array is NULL", name);
+  if (st[3] != 1) return fail(CIE_EINVAL, "%s: head_dim stride must be 1, got %lld", name, (long long)st[3]);
+  for (int i = 0; i < 3; ++i) {
+    if (st[i] < 0) return fail(CIE_EINVAL, "%s: negative stride %lld", name, (long long)st[i]);
+    if (st[i] % 8) return fail(CIE_EINVAL, "%s: stride %lld is not a multiple of 8 elements", name, (long long)st[i]);
+  }
+  return CIE_OK;
+}
+
+int check_ptr(const char* name, const void* ptr) {
+  if (!ptr) return fail(CIE_EINVAL, "%s: NULL pointer", name);
+  if (!aligned16(ptr)) return fail(CIE_EINVAL, "%s: pointer is not 16-byte aligned", name);
+  return CIE_OK;
+}
+
+int common_checks(int Hq, int Hk, int D, int dtype) {
+  if (dtype != CIE_DTYPE_F16 && dtype != CIE_DTYPE_BF16)
+    return fail(CIE_EDTYPE, "unsupported dtype code %d (f16 = 0, bf16 = 1)", dtype);
+  if (!head_dim_ok(D))
+    return fail(CIE_EHEADDIM, "head_dim must be a power of 2 in [16, 256], got %d", D);
+  if (Hq < 1 || Hk < 1) return fail(CIE_EINVAL, "head counts must be positive (Hq=%d, Hk=%d)", Hq, Hk);
+  if (Hq % Hk) return fail(CIE_EINVAL, "num_heads %d must be a multiple of num_kv_heads %d", Hq, Hk);
+  return CIE_OK;
+}
+
+int launch_status(hipError_t e) {
+  if (e != hipSuccess) return fail(CIE_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  g_err.clear();
+  return CIE_OK;
+}
+
+#define CIE_TRY(x)             \
+  do {                         \
+    int _rc = (x);             \
+    if (_rc != CIE_OK) return _rc; \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int cie_abi_version(void) { return CIE_ABI_VERSION; }
+
+const char* cie_last_error(void) { return g_err.c_str(); }
+
+int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
+                  const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride,
+                  int B, int Hq, int Hk, int Lq, int Lk, int D,
+                  float scale, int causal, int dtype, void* stream) {
+  CIE_TRY(common_checks(Hq, Hk, D, dtype));
+  if (B < 0 || Lq < 0 || Lk < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d, Lk=%d)", B, Lq, Lk);
+  if (!std::isfinite(scale)) return fail(CIE_EINVAL, "scale must be finite");
+  if ((int64_t)B * Hq * Lq == 0) {
+    g_err.clear();
+    return CIE_OK;  // empty output: nothing to compute
+  }
+  CIE_TRY(check_ptr("q", q));
+  CIE_TRY(check_ptr("o", o));
+  CIE_TRY(check_strides("q", q_stride));
+  CIE_TRY(check_strides("o", o_stride));
+  if (Lk > 0) {
+    CIE_TRY(check_ptr("k", k));
+    CIE_TRY(check_ptr("v", v));
+    CIE_TRY(check_strides("k", k_stride));
+    CIE_TRY(check_strides("v", v_stride));
+  }
+  const int64_t n_mt = ((int64_t)Lq + 127) / 128;
+  const int64_t n_wg = n_mt * B * Hq;
+  if (n_wg > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
+
+  cie::FlashParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<uint16_t*>(o);
+  p.qs0 = q_stride[0]; p.qs1 = q_stride[1]; p.qs2 = q_stride[2];
+  p.os0 = o_stride[0]; p.os1 = o_stride[1]; p.os2 = o_stride[2];
+  if (Lk > 0) {
+    p.ks0 = k_stride[0]; p.ks1 = k_stride[1]; p.ks2 = k_stride[2];
+    p.vs0 = v_stride[0]; p.vs1 = v_stride[1]; p.vs2 = v_stride[2];
+  }
+  p.B = B; p.Hq = Hq; p.Hk = Hk; p.Lq = Lq; p.Lk = Lk; p.group = Hq / Hk;
+  p.n_mt = (int)n_mt;
+  p.n_wg = (int)n_wg;
+  p.scale_log2 = scale * cie::kLog2e;
+  p.causal = causal ? 1 : 0;
+  return launch_status(cie::launch_flash(p, dtype, D, static_cast<hipStream_t>(stream)));
+}
+
+static int paged_geometry(int B, int Hq, int Hk, int Lq, int max_context, int block_size,
+                          int max_blocks_per_seq, int* split_len, int* n_splits) {
+  const int64_t bound = (int64_t)max_blocks_per_seq * block_size;
+  int64_t mc = max_context > 0 ? std::min<int64_t>(max_context, bound) : bound;
+  if (mc < 1) mc = 1;
+  const int R = (Hq / Hk) * Lq;
+  const int n_qt = (R + 31) / 32;
+  *split_len = cie::paged_split_len(B, Hk, n_qt, (int)mc);
+  *n_splits = (int)((mc + *split_len - 1) / *split_len);
+  return CIE_OK;
+}
+
+size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D, int max_context,
+                                 int block_size, int max_blocks_per_seq) {
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Lq <= 0 || D <= 0 || block_size <= 0 || max_blocks_per_seq < 0 ||
+      Hq % Hk)
+    return 0;
+  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff) return 0;
+  int split_len = 0, n_splits = 0;
+  paged_geometry(B, Hq, Hk, Lq, max_context, block_size, max_blocks_per_seq, &split_len, &n_splits);
+  if (n_splits <= 1) return 0;
+  return (size_t)B * Hq * Lq * n_splits * (D + 2) * sizeof(float);
+}
+
+int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
+                  const int32_t* block_tables, const int32_t* context_lens,
+                  void* o, void* workspace, size_t workspace_bytes,
+                  const int64_t* q_stride, const int64_t* kc_stride,
+                  const int64_t* vc_stride, const int64_t* o_stride,
+                  int B, int Hq, int Hk, int Lq, int D,
+                  int num_blocks, int block_size, int max_blocks_per_seq,
+                  int max_context, float scale, int causal, int dtype,
+                  void* stream) {
+  CIE_TRY(common_checks(Hq, Hk, D, dtype));
+  if (B < 0 || Lq < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d)", B, Lq);
+  if (block_size < 1) return fail(CIE_EINVAL, "block_size must be positive, got %d", block_size);
+  if (num_blocks < 0 || max_blocks_per_seq < 0)
+    return fail(CIE_EINVAL, "negative pool geometry (num_blocks=%d, max_blocks_per_seq=%d)", num_blocks,
+                max_blocks_per_seq);
+  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff)
+    return fail(CIE_EINVAL, "max_blocks_per_seq * block_size exceeds 2^31");
+  if (!std::isfinite(scale)) return fail(CIE_EINVAL, "scale must be finite");
+  if ((int64_t)B * Hq * Lq == 0) {
+    g_err.clear();
+    return CIE_OK;
+  }
+  CIE_TRY(check_ptr("q", q));
+  CIE_TRY(check_ptr("o", o));
+  CIE_TRY(check_ptr("k_cache", k_cache));
+  CIE_TRY(check_ptr("v_cache", v_cache));
+  if (!block_tables || !context_lens) return fail(CIE_EINVAL, "block_tables / context_lens: NULL pointer");
+  CIE_TRY(check_strides("q", q_stride));
+  CIE_TRY(check_strides("o", o_stride));
+  CIE_TRY(check_strides("k_cache", kc_stride));
+  CIE_TRY(check_strides("v_cache", vc_stride));
+  if ((int64_t)B * Hk > 65535) return fail(CIE_EINVAL, "batch * num_kv_heads exceeds 65535");
+
+  cie::PagedParams p{};
+  int split_len = 0, n_splits = 0;
+  paged_geometry(B, Hq, Hk, Lq, max_context, block_size, max_blocks_per_seq, &split_len, &n_splits);
+  const size_t need = n_splits > 1 ? (size_t)B * Hq * Lq * n_splits * (D + 2) * sizeof(float) : 0;
+  if (need) {
+    if (!workspace || workspace_bytes < need)
+      return fail(CIE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(CIE_EINVAL, "workspace: pointer is not 16-byte aligned");
+    p.ws_acc = static_cast<float*>(workspace);
+    p.ws_ml = p.ws_acc + (size_t)B * Hq * Lq * n_splits * D;
+  }
+  const int R = (Hq / Hk) * Lq;
+  if ((R + 31) / 32 > 65535) return fail(CIE_EINVAL, "too many query rows per kv head (%d)", R);
+
+  p.q = static_cast<const uint16_t*>(q);
+  p.kc = static_cast<const uint16_t*>(k_cache);
+  p.vc = static_cast<const uint16_t*>(v_cache);
+  p.o = static_cast<uint16_t*>(o);
+  p.bt = block_tables;
+  p.lens = context_lens;
+  p.qs0 = q_stride[0]; p.qs1 = q_stride[1]; p.qs2 = q_stride[2];
+  p.ks0 = kc_stride[0]; p.ks1 = kc_stride[1]; p.ks2 = kc_stride[2];
+  p.vs0 = vc_stride[0]; p.vs1 = vc_stride[1]; p.vs2 = vc_stride[2];
+  p.os0 = o_stride[0]; p.os1 = o_stride[1]; p.os2 = o_stride[2];
+  p.B = B; p.Hq = Hq; p.Hk = Hk; p.Lq = Lq; p.group = Hq / Hk; p.R = R;
+  p.num_blocks = num_blocks;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_size = block_size;
+  p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
+  p.split_len = split_len;
+  p.n_splits = n_splits;
+  p.scale_log2 = scale * cie::kLog2e;
+  p.causal = causal ? 1 : 0;
+  return launch_status(cie::launch_paged(p, dtype, D, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

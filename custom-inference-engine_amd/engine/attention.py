@@ -1,0 +1,173 @@
+"""Attention entry points: the drop-in for the reference's ``engine/attention.py``.
+
+``flash_attention`` keeps the reference signature and argument checks
+(``engine/attention.py:6-32``) and runs the gfx950 prefill kernel of
+``libcie_attn.so``. ``paged_attention`` is the added entry that attends
+straight out of the paged KV pool (``engine/cache/kv_cache.py:55``) through
+int32 block tables, replacing ``cache.gather`` + dense attention
+(``engine/model/block.py:56-71``).
+
+Both accept fp16 and bf16 (the reference accepts fp16 only,
+``engine/attention.py:24-25``); scores, softmax and accumulation run in fp32.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from engine import _lib
+
+_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def _check_head_dim(D: int) -> None:
+    if D & (D - 1):
+        raise ValueError(f"head_dim must be power of 2, got {D}")
+    if D < 16:
+        raise ValueError(f"head_dim must be >= 16, got {D}")
+    if D > 256:
+        raise ValueError(f"head_dim must be <= 256, got {D}")
+
+
+def _check_dtype(t: torch.Tensor) -> None:
+    if t.dtype not in _DTYPES:
+        raise ValueError(f"attention kernels expect FP16 or BF16 Q/K/V, got {t.dtype}")
+
+
+def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` unchanged when the kernels can read it in place (unit
+    head_dim stride, 16-byte aligned rows); otherwise a contiguous copy."""
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+        t.shape[i] == 1 or t.stride(i) % 8 == 0 for i in range(t.dim() - 1))
+    if ok:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
+def flash_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Flash attention on the GPU.
+
+    Shapes: q (B, H, M, D); k/v (B, Hk, N, D) with H % Hk == 0 (GQA: query
+    head h reads kv head h // (H // Hk)). ``causal`` masks bottom-right
+    aligned: row i sees keys j <= N - M + i. ``scale`` defaults to
+    1/sqrt(D). Returns a new contiguous (B, H, M, D) tensor in q's dtype.
+    """
+    if not q.is_cuda:
+        raise RuntimeError("flash_attention requires CUDA tensors")
+    if not (k.is_cuda and v.is_cuda) or k.device != q.device or v.device != q.device:
+        raise RuntimeError("flash_attention requires q, k, v on the same CUDA device")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("flash_attention expects 4-d q (B,H,M,D) and k/v (B,Hk,N,D)")
+    D = q.shape[-1]
+    _check_head_dim(D)
+    _check_dtype(q)
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    B, H, M, _ = q.shape
+    Bk, Hk, N, Dk = k.shape
+    if tuple(v.shape) != tuple(k.shape) or Bk != B or Dk != D:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if Hk < 1 or H % Hk:
+        raise ValueError(f"num_heads {H} must be a multiple of num_kv_heads {Hk}")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+
+    lib = _lib.load()
+    q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
+    out = torch.empty((B, H, M, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.cie_flash_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
+            B, H, Hk, M, N, D, float(scale), 1 if causal else 0,
+            _lib.DTYPE_CODES[q.dtype], _lib.stream_handle(q.device))
+    _lib.check(rc)
+    return out
+
+
+def paged_workspace_bytes(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size: int,
+                          max_blocks_per_seq: int, max_context: int | None = None) -> int:
+    """Device workspace (bytes) a :func:`paged_attention` call of this shape
+    needs for its context-split partials."""
+    return int(_lib.load().cie_paged_workspace_bytes(
+        B, Hq, Hk, Lq, D, int(max_context or 0), block_size, max_blocks_per_seq))
+
+
+def paged_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    causal: bool = True,
+    scale: float | None = None,
+    max_context: int | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention of the newest ``Lq`` tokens of each sequence over its paged
+    KV history.
+
+    q: (B, Hq, Lq, D). k_cache / v_cache: one layer's pool,
+    (num_blocks, block_size, Hk, D). block_tables: int32 (B, max_blocks),
+    row b = the physical block ids of sequence b in logical order.
+    context_lens: int32 (B,), tokens in the pool per sequence including the
+    Lq new ones (the reference appends before attending). With ``causal``
+    new token i sees positions <= context_len - Lq + i. ``max_context`` (an
+    upper bound of context_lens) lets the launch size its context splits
+    tighter than max_blocks * block_size. Equal to ``flash_attention`` over
+    ``cache.gather`` per sequence. Returns (B, Hq, Lq, D) in q's dtype.
+    """
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("block_tables", block_tables), ("context_lens", context_lens)):
+        if not t.is_cuda or t.device != q.device:
+            raise RuntimeError(f"paged_attention requires CUDA tensors on one device ({name})")
+    if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("paged_attention expects q (B,Hq,Lq,D) and pools (num_blocks,block_size,Hk,D)")
+    D = q.shape[-1]
+    _check_head_dim(D)
+    _check_dtype(q)
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError(f"q and the KV pool must share a dtype, got {q.dtype}, {k_cache.dtype}, {v_cache.dtype}")
+    if tuple(k_cache.shape) != tuple(v_cache.shape) or k_cache.shape[-1] != D:
+        raise ValueError(f"pool shape mismatch: k {tuple(k_cache.shape)}, v {tuple(v_cache.shape)}, head_dim {D}")
+    B, Hq, Lq, _ = q.shape
+    num_blocks, block_size, Hk, _ = k_cache.shape
+    if Hk < 1 or Hq % Hk:
+        raise ValueError(f"num_heads {Hq} must be a multiple of num_kv_heads {Hk}")
+    if block_tables.dim() != 2 or block_tables.shape[0] != B:
+        raise ValueError(f"block_tables must be (B, max_blocks), got {tuple(block_tables.shape)}")
+    if context_lens.dim() != 1 or context_lens.shape[0] != B:
+        raise ValueError(f"context_lens must be (B,), got {tuple(context_lens.shape)}")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+
+    lib = _lib.load()
+    bt = block_tables.to(torch.int32).contiguous()
+    lens = context_lens.to(torch.int32).contiguous()
+    max_blocks = bt.shape[1]
+    q = _kernel_layout(q)
+    k_cache, v_cache = _kernel_layout(k_cache), _kernel_layout(v_cache)
+    mc = int(max_context or 0)
+    ws_bytes = int(lib.cie_paged_workspace_bytes(B, Hq, Hk, Lq, D, mc, block_size, max_blocks))
+    if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    out = torch.empty((B, Hq, Lq, D), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.cie_paged_fwd(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(),
+            out.data_ptr(),
+            workspace.data_ptr() if ws_bytes else None,
+            ws_bytes,
+            _lib.strides(q), _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out),
+            B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc,
+            float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype], _lib.stream_handle(q.device))
+    _lib.check(rc)
+    return out

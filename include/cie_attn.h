@@ -1,0 +1,117 @@
+/*
+ * cie_attn.h - C ABI of the MI355X (gfx950) attention library `libcie_attn.so`.
+ *
+ * Two entry points carry the attention hot path of the engine:
+ *
+ *   cie_flash_fwd   dense (prefill) attention. Replaces the Triton launch behind
+ *                   engine/attention.py:6-32 -> kernels/flash_attention.py:136-209
+ *                   (kernel kernels/flash_attention.py:21-120).
+ *   cie_paged_fwd   decode / speculative-verify attention that reads K and V
+ *                   straight out of the paged pool through the block table.
+ *                   Replaces the gather-then-dense sequence of
+ *                   engine/model/block.py:56-71 (cache.gather at
+ *                   engine/cache/kv_cache.py:141-165 followed by flash_attention).
+ *
+ * Conventions shared by every entry point:
+ *   - Every pointer is a device pointer (e.g. torch.Tensor.data_ptr()).
+ *   - Strides are in elements, four per tensor, outermost first. The innermost
+ *     (head_dim) stride must be 1; every other stride is free, so transposed
+ *     views such as the (1, Hk, N, D) view of a gathered (N, Hk, D) history
+ *     need no copy.
+ *   - `stream` is a hipStream_t (0 = null stream). Work is enqueued
+ *     asynchronously; nothing synchronises, allocates or frees.
+ *   - Return value 0 means success; a negative CIE_E* code means nothing was
+ *     enqueued and cie_last_error() holds a message (thread-local).
+ *   - dtype: CIE_DTYPE_F16 or CIE_DTYPE_BF16 for q, k, v and the output alike.
+ *   - Semantics follow kernels/ref/flash_attention_ref.py:8-56: query head h
+ *     reads kv head h / (Hq / Hk); with causal != 0 query row i sees key j iff
+ *     j <= Lk - Lq + i (bottom-right aligned); scores and the softmax run in
+ *     fp32, the probabilities are rounded to the input dtype before P.V, and
+ *     the result is written in the input dtype. A row with keys but none
+ *     visible is NaN; Lk == 0 gives zeros.
+ */
+#ifndef CIE_ATTN_H
+#define CIE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CIE_ABI_VERSION 1
+
+enum cie_dtype { CIE_DTYPE_F16 = 0, CIE_DTYPE_BF16 = 1 };
+
+enum cie_status {
+  CIE_OK = 0,
+  CIE_EINVAL = -1,       /* bad pointer, negative size, bad stride, H % Hk != 0 */
+  CIE_EHEADDIM = -2,     /* head_dim not a power of two in [16, 256]            */
+  CIE_EDTYPE = -3,       /* dtype other than f16 / bf16                         */
+  CIE_EWORKSPACE = -4,   /* paged workspace missing or too small                */
+  CIE_ELAUNCH = -5       /* the HIP runtime refused the launch                  */
+};
+
+/* ABI version compiled into the library (CIE_ABI_VERSION). */
+int cie_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* cie_last_error(void);
+
+/*
+ * Dense attention: o = softmax(q k^T * scale [+ causal mask]) v.
+ *   q: (B, Hq, Lq, D)   k, v: (B, Hk, Lk, D)   o: (B, Hq, Lq, D)
+ * Reference: engine/attention.py:6-32 (argument checks :17-25, call :27-32)
+ * and kernels/flash_attention.py:136-209 (GQA mapping :150-155, default scale
+ * :157-158 -- the caller passes the resolved scale here).
+ */
+int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
+                  const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride,
+                  int B, int Hq, int Hk, int Lq, int Lk, int D,
+                  float scale, int causal, int dtype, void* stream);
+
+/*
+ * Bytes of device workspace cie_paged_fwd needs for this shape (may be 0).
+ * max_context bounds every context_lens[b]; pass <= 0 to use the table bound
+ * max_blocks_per_seq * block_size (the value cie_paged_fwd uses the same way).
+ * No reference counterpart: the reference never splits a context.
+ */
+size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D,
+                                 int max_context, int block_size,
+                                 int max_blocks_per_seq);
+
+/*
+ * Paged attention over the engine's KV pool.
+ *   q: (B, Hq, Lq, D) -- the Lq newest tokens of each sequence
+ *   k_cache, v_cache: (num_blocks, block_size, Hk, D), the per-layer pool
+ *        layout of engine/cache/kv_cache.py:55-63
+ *   block_tables: int32 [B, max_blocks_per_seq], row b = BlockTable.blocks of
+ *        sequence b (engine/cache/block_table.py:16-18); token t of sequence b
+ *        lives at pool[block_tables[b][t / block_size], t % block_size]
+ *        (engine/cache/block_table.py:23-26)
+ *   context_lens: int32 [B], tokens already in the pool for each sequence,
+ *        the Lq new ones included (the reference appends before it attends,
+ *        engine/model/block.py:57-65)
+ *   o: (B, Hq, Lq, D)
+ * Equals flash_attention_ref(q[b], gather(b), causal, scale) per sequence.
+ * A block id outside [0, num_blocks) or a context length outside
+ * [0, max_blocks_per_seq * block_size] is never dereferenced: the affected
+ * sequence's output is written as NaN instead.
+ */
+int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
+                  const int32_t* block_tables, const int32_t* context_lens,
+                  void* o, void* workspace, size_t workspace_bytes,
+                  const int64_t* q_stride, const int64_t* kc_stride,
+                  const int64_t* vc_stride, const int64_t* o_stride,
+                  int B, int Hq, int Hk, int Lq, int D,
+                  int num_blocks, int block_size, int max_blocks_per_seq,
+                  int max_context, float scale, int causal, int dtype,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CIE_ATTN_H */

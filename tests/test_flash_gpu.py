@@ -1,0 +1,175 @@
+"""GPU parity of the prefill kernel (engine.attention.flash_attention ->
+cie_flash_fwd) against the CPU oracle.
+
+Bar: max |out - ref| <= 2e-3 for fp16 and <= 1e-2 for bf16, where ref is the
+fp32 oracle evaluated on the same rounded inputs; NaN patterns must agree.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from benchmarks import workloads
+from engine.attention import flash_attention
+from oracle import attention_rows_ref, flash_attention_ref, flash_attention_ref_chunked
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
+DEV = "cuda"
+
+
+def assert_close(out: torch.Tensor, ref: torch.Tensor, tol: float, what: str = "") -> float:
+    out = out.float().cpu()
+    ref = ref.float().cpu()
+    assert out.shape == ref.shape, (out.shape, ref.shape)
+    n_out, n_ref = torch.isnan(out), torch.isnan(ref)
+    assert torch.equal(n_out, n_ref), f"{what}: NaN pattern differs ({int(n_out.sum())} vs {int(n_ref.sum())})"
+    ok = ~n_ref
+    err = float((out[ok] - ref[ok]).abs().max()) if ok.any() else 0.0
+    assert err <= tol, f"{what}: max abs error {err:.3e} > {tol:.1e}"
+    return err
+
+
+def _inputs(B, H, Hk, Lq, Lk, D, dtype, seed, vscale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Lq, D, generator=g).to(dtype)
+    k = torch.randn(B, Hk, Lk, D, generator=g).to(dtype)
+    v = (torch.randn(B, Hk, Lk, D, generator=g) * vscale).to(dtype)
+    return q, k, v
+
+
+def test_reference_kernel_case():
+    # the reference's kernel test: fp16 (2,4,64,64,64), causal, seed 0
+    torch.manual_seed(0)
+    q = torch.randn(2, 4, 64, 64, device=DEV, dtype=torch.float16)
+    k = torch.randn(2, 4, 64, 64, device=DEV, dtype=torch.float16)
+    v = torch.randn(2, 4, 64, 64, device=DEV, dtype=torch.float16)
+    out = flash_attention(q, k, v, causal=True)
+    ref = flash_attention_ref(q.cpu().float(), k.cpu().float(), v.cpu().float(), causal=True)
+    assert out.dtype == torch.float16 and out.shape == q.shape and out.is_contiguous()
+    assert_close(out, ref, 2e-3, "reference case")
+
+
+SHAPES = [
+    # B, H, Hk, Lq, Lk
+    (1, 4, 2, 77, 77),      # ragged single tile
+    (2, 8, 2, 33, 200),     # prefill over a cache (Lq < Lk)
+    (1, 4, 4, 130, 130),    # MHA, two query tiles
+    (1, 6, 3, 300, 311),    # several tiles, ragged key tail
+]
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_sweep(D, dtype, causal, shape):
+    B, H, Hk, Lq, Lk = shape
+    q, k, v = _inputs(B, H, Hk, Lq, Lk, D, dtype, seed=D + Lq + Lk, vscale=0.5)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=causal)
+    assert_close(out, ref, TOL[dtype], f"D={D} {dtype} causal={causal} {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_more_queries_than_keys_gives_nan_rows(dtype):
+    q, k, v = _inputs(1, 4, 2, 150, 20, 64, dtype, seed=5, vscale=0.5)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=True)
+    assert torch.isnan(ref[:, :, :130]).all()
+    assert_close(out, ref, TOL[dtype], "Lq > Lk")
+
+
+def test_empty_history_gives_zeros():
+    q, k, v = _inputs(1, 4, 2, 5, 0, 64, torch.float16, seed=6)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    assert (out == 0).all()
+
+
+def test_empty_query():
+    q, k, v = _inputs(1, 4, 2, 0, 9, 64, torch.float16, seed=7)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    assert out.shape == (1, 4, 0, 64)
+
+
+def test_strided_views_match_contiguous():
+    # the call-site layout: gathered (N, Hk, D) history viewed as (1, Hk, N, D)
+    g = torch.Generator().manual_seed(8)
+    N, Hk, H, D, L = 97, 2, 8, 64, 97
+    hist_k = torch.randn(N, Hk, D, generator=g).half().to(DEV)
+    hist_v = torch.randn(N, Hk, D, generator=g).half().to(DEV)
+    q = torch.randn(1, L, H, D, generator=g).half().to(DEV).transpose(1, 2)  # (1, H, L, D) view
+    kv_k = hist_k.transpose(0, 1).unsqueeze(0)
+    kv_v = hist_v.transpose(0, 1).unsqueeze(0)
+    assert not kv_k.is_contiguous() and not q.is_contiguous()
+    out = flash_attention(q, kv_k, kv_v, causal=True, scale=1.0 / math.sqrt(D))
+    out_c = flash_attention(q.contiguous(), kv_k.contiguous(), kv_v.contiguous(), causal=True)
+    assert torch.equal(out, out_c)
+
+
+def test_gqa_equals_expanded_mha_bitwise():
+    q, k, v = _inputs(2, 8, 2, 100, 140, 64, torch.float16, seed=9)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    gqa = flash_attention(q, k, v, causal=True)
+    mha = flash_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), causal=True)
+    assert torch.equal(gqa, mha)
+
+
+def test_deterministic():
+    q, k, v = _inputs(1, 8, 2, 257, 257, 128, torch.bfloat16, seed=10)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    assert torch.equal(flash_attention(q, k, v, causal=True), flash_attention(q, k, v, causal=True))
+
+
+def test_explicit_scale():
+    q, k, v = _inputs(1, 4, 2, 64, 64, 64, torch.float16, seed=11)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=False, scale=0.05)
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=False, scale=0.05)
+    assert_close(out, ref, 2e-3, "scale=0.05")
+
+
+def test_boundary_errors_match_reference_types():
+    q = torch.randn(1, 2, 4, 16, device=DEV, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        flash_attention(q.float(), q.float(), q.float())
+    bad = torch.randn(1, 2, 4, 24, device=DEV, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        flash_attention(bad, bad, bad)
+    small = torch.randn(1, 2, 4, 8, device=DEV, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        flash_attention(small, small, small)
+    with pytest.raises(ValueError):
+        flash_attention(q, q[:, :1].repeat(1, 3, 1, 1)[:, :3], q[:, :1].repeat(1, 3, 1, 1)[:, :3])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_workload_prefill_s128(dtype):
+    # the CPU-oracle workload, run on the GPU in fp16 and bf16
+    case = workloads.prefill_s128()
+    q, k, v = case.q.to(dtype), case.k.to(dtype), case.v.to(dtype)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=True)
+    assert_close(out, ref, TOL[dtype], f"prefill_s128 {dtype}")
+
+
+def test_workload_prefill_s2048():
+    case = workloads.prefill_s2048()
+    out = flash_attention(case.q.to(DEV), case.k.to(DEV), case.v.to(DEV), causal=True)
+    ref = flash_attention_ref_chunked(case.q, case.k, case.v, causal=True, q_chunk=1024)
+    assert_close(out, ref, 2e-3, "prefill_s2048")
+
+
+def test_workload_prefill_s16384_sampled_rows():
+    case = workloads.prefill_s16384()
+    out = flash_attention(case.q.to(DEV), case.k.to(DEV), case.v.to(DEV), causal=True).cpu()
+    assert not torch.isnan(out).any()
+    # causal row 0 attends to key 0 alone: P = 1 exactly, so the row is V[kv(h), 0] bit for bit
+    assert torch.equal(out[0, :, 0], case.v[0, torch.arange(32) // 4, 0])
+    g = torch.Generator().manual_seed(123)
+    rows = [1, 127, 128, 129, 4095, 8191, 16383] + torch.randint(0, 16384, (25,), generator=g).tolist()
+    ref = attention_rows_ref(case.q, case.k, case.v, rows, causal=True)
+    assert_close(out[:, :, rows], ref, 1e-2, "prefill_s16384 sampled rows")
