@@ -4,6 +4,7 @@
 // (engine/attention.py:17-25, kernels/flash_attention.py:147-165) and turns
 // them into status codes; the Python layer maps the codes back onto the
 // reference's exception types.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdarg>
@@ -64,6 +65,14 @@ int launch_status(hipError_t e) {
   return CIE_OK;
 }
 
+// Kernels compute exp2(s * c - m) with c = |scale| * log2(e) >= 0; a negative
+// scale is folded into an exact sign flip of q (s * scale = (-q).k * |scale|).
+// A zero scale becomes a tiny positive one (uniform weights either way).
+void set_scale(float scale, float* c, uint32_t* q_sign) {
+  *q_sign = scale < 0.f ? 0x80008000u : 0u;
+  *c = std::max(std::fabs(scale) * cie::kLog2e, 1e-30f);
+}
+
 #define CIE_TRY(x)             \
   do {                         \
     int _rc = (x);             \
@@ -118,7 +127,7 @@ int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
   p.B = B; p.Hq = Hq; p.Hk = Hk; p.Lq = Lq; p.Lk = Lk; p.group = Hq / Hk;
   p.n_mt = (int)n_mt;
   p.n_wg = (int)n_wg;
-  p.scale_log2 = scale * cie::kLog2e;
+  set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
   return launch_status(cie::launch_flash(p, dtype, D, static_cast<hipStream_t>(stream)));
 }
@@ -130,7 +139,7 @@ static int paged_geometry(int B, int Hq, int Hk, int Lq, int max_context, int bl
   if (mc < 1) mc = 1;
   const int R = (Hq / Hk) * Lq;
   const int n_qt = (R + 31) / 32;
-  *split_len = cie::paged_split_len(B, Hk, n_qt, (int)mc);
+  *split_len = cie::paged_split_len(B, Hk, n_qt, (int)mc, block_size);
   *n_splits = (int)((mc + *split_len - 1) / *split_len);
   return CIE_OK;
 }
@@ -178,7 +187,6 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   CIE_TRY(check_strides("o", o_stride));
   CIE_TRY(check_strides("k_cache", kc_stride));
   CIE_TRY(check_strides("v_cache", vc_stride));
-  if ((int64_t)B * Hk > 65535) return fail(CIE_EINVAL, "batch * num_kv_heads exceeds 65535");
 
   cie::PagedParams p{};
   int split_len = 0, n_splits = 0;
@@ -193,7 +201,8 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
     p.ws_ml = p.ws_acc + (size_t)B * Hq * Lq * n_splits * D;
   }
   const int R = (Hq / Hk) * Lq;
-  if ((R + 31) / 32 > 65535) return fail(CIE_EINVAL, "too many query rows per kv head (%d)", R);
+  const int n_qt = (R + 31) / 32;
+  if ((int64_t)B * n_splits * n_qt * Hk > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
 
   p.q = static_cast<const uint16_t*>(q);
   p.kc = static_cast<const uint16_t*>(k_cache);
@@ -212,7 +221,8 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
   p.split_len = split_len;
   p.n_splits = n_splits;
-  p.scale_log2 = scale * cie::kLog2e;
+  p.n_qt = n_qt;
+  set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
   return launch_status(cie::launch_paged(p, dtype, D, static_cast<hipStream_t>(stream)));
 }

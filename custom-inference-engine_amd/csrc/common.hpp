@@ -93,10 +93,27 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
 }
 
 // 16-byte global load that yields zeros when !ok (no memory access then).
+// Used outside the streaming loops; the loops use load16_clamped.
 __device__ __forceinline__ u32x4 load16(const uint16_t* p, bool ok) {
   u32x4 r = {0u, 0u, 0u, 0u};
   if (ok) r = *reinterpret_cast<const u32x4*>(p);
   return r;
+}
+
+// Unconditional 16-byte load from an address the caller has already clamped
+// into the tensor. No branch, so the compiler keeps the loads of a whole tile
+// in flight together and waits only where the data is consumed.
+__device__ __forceinline__ u32x4 load16_clamped(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Same, marked non-temporal: for data read exactly once (the paged KV pool).
+__device__ __forceinline__ u32x4 load16_stream(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ u32x4 zero_unless(u32x4 v, bool ok) {
+  return u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
 }
 
 // Transpose helpers for 16-bit data held two per dword: from four rows

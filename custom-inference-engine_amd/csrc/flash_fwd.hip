@@ -9,45 +9,52 @@
 // Per K/V tile of BN keys and per wave:
 //   S^T[BN x 32] = K_tile . Q_w^T        MFMA 32x32x16, K from LDS (row-major),
 //                                          Q^T resident in registers
-//   mask + running max (one v_permlane32_swap), p = exp2(s*scale*log2e - m)
+//   mask + running max (one v_permlane32_swap), p = exp2(s*c - m), c = scale*log2e
 //   O^T[D x 32] += V^T_tile . P^T         MFMA 32x32x16, V^T from LDS, P^T
 //                                          straight from the S^T registers
 // The bottom-right causal rule (key j visible to row i iff j <= Lk - Lq + i,
 // kernels/flash_attention.py:99-102) is applied only on tiles that cross a
 // wave's diagonal or the key tail; a workgroup stops at the last key any of
 // its rows can see (the n_end bound of kernels/flash_attention.py:75-77).
+//
+// The running max is refreshed lazily: a row keeps its reference max m until
+// a tile raises the row max by more than 2^8 (so p <= 256, exact to fp16 /
+// bf16 rounding), and the accumulator rescale is skipped for the whole wave
+// when no row needs it. The final acc / l is unchanged by the choice of m.
 #include "kernels.hpp"
 
 namespace cie {
 
+constexpr float kLazyRescale = 8.0f;  // log2 of the largest p tolerated before rescaling
+
 template <int D>
 struct FlashCfg {
-  static constexpr int BM = 128;                                 // query rows per workgroup
-  static constexpr int BN = D <= 64 ? 128 : (D == 128 ? 64 : 32);  // keys per tile
-  static constexpr int KSTR = D + 8;                             // LDS row pitch of K (elements)
-  static constexpr int VSTR = BN + 4;                            // LDS row pitch of V^T (elements)
-  static constexpr int DT = D >= 32 ? D / 32 : 1;                // 32-row output tiles
-  static constexpr int KK = D / 16;                              // MFMA steps over head_dim
-  static constexpr int MT = BN / 32;                             // 32-key score tiles
+  static constexpr int BM = 128;                                            // query rows per workgroup
+  static constexpr int BN = D <= 32 ? 128 : (D <= 128 ? 64 : 32);           // keys per tile
+  static constexpr int KSTR = D + 8;                                        // LDS row pitch of K
+  static constexpr int VSTR = BN + 4;                                       // LDS row pitch of V^T
+  static constexpr int DT = D >= 32 ? D / 32 : 1;                           // 32-row output tiles
+  static constexpr int KK = D / 16;                                         // MFMA steps over head_dim
+  static constexpr int MT = BN / 32;                                        // 32-key score tiles
   static constexpr int KBUF = BN * KSTR;
   static constexpr int VBUF = D * VSTR;
-  static constexpr int BUF = KBUF + VBUF;                        // elements per LDS stage
-  static constexpr int KCH = BN * D / 8 / 256;                   // 16-byte K chunks per thread
-  static constexpr int VGR = (BN / 4) * (D / 8);                 // 4-key x 8-dim V groups
-  static constexpr int VG = (VGR + 255) / 256;                   // V groups per thread
+  static constexpr int BUF = KBUF + VBUF;                                   // elements per LDS stage
+  static constexpr int KCH = BN * D / 8 / 256;                              // 16-byte K chunks per thread
+  static constexpr int VGR = (BN / 4) * (D / 8);                            // 4-key x 8-dim V groups
+  static constexpr int VG = (VGR + 255) / 256;                              // V groups per thread
   static_assert(KCH >= 1 && BN * D / 8 == KCH * 256, "K tile must split evenly over 256 threads");
 };
 
 template <int DTYPE, int D>
-__global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
+__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(const FlashParams p) {
   using C = FlashCfg<D>;
   using E = Elt<DTYPE>;
   constexpr int BN = C::BN;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * C::BUF];
 
   // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
-  // contiguous run of logical tiles so the 4 query heads of a kv head (and
-  // its neighbouring query tiles) share one L2. Within a kv head the longest
+  // contiguous run of logical tiles so the query heads of a kv head (and its
+  // neighbouring query tiles) share one L2. Within a kv head the longest
   // (last) query tiles go first.
   const int N = p.n_wg;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -65,13 +72,17 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
   const int q0w = mt * C::BM + wave * 32;  // first row of this wave
   const int qi = q0w + l32;                // row owned by this lane
 
-  // Q^T as the B operand: lane holds Q[qi][16kk + 8hl .. +8].
+  // Q^T as the B operand: lane holds Q[qi][16kk + 8hl .. +8] (sign-flipped
+  // when the caller's scale is negative, so c below is never negative).
   const uint16_t* qrow = p.q + b * p.qs0 + hq * p.qs1 + (int64_t)qi * p.qs2;
   u32x4 qf[C::KK];
 #pragma unroll
-  for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
+  for (int kk = 0; kk < C::KK; ++kk) {
+    qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
+    qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
+  }
 
-  // Key range of the workgroup and of this wave.
+  // Key range of the workgroup and of this wave; lim = last key this row sees.
   const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;
   int kend = p.Lk;
   if (p.causal) kend = max(0, min(p.Lk, p.Lk - p.Lq + wg_last_row + 1));
@@ -80,54 +91,62 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
     wave_kend = p.Lk;
     if (p.causal) wave_kend = max(0, min(p.Lk, p.Lk - p.Lq + min(q0w + 31, p.Lq - 1) + 1));
   }
-  const int wave_diag0 = p.Lk - p.Lq + q0w;  // last visible key of the wave's first row
-  const int diag = p.Lk - p.Lq + qi;         // last visible key of this lane's row
+  const int lim = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + qi) : p.Lk - 1;
+  const int wave_lim0 = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + q0w) : p.Lk - 1;  // smallest lim in the wave
   const int n_tiles = (kend + BN - 1) / BN;
+  const float c = p.scale_log2;
 
   const uint16_t* kb = p.k + b * p.ks0 + kvh * p.ks1;
   const uint16_t* vb = p.v + b * p.vs0 + kvh * p.vs1;
+  const int last_key = max(p.Lk - 1, 0);
 
   u32x4 kreg[C::KCH];
   u32x4 vreg[C::VG][4];
+  uint32_t vok[C::VG];  // bit r: key 4*p4 + r of the group exists
   auto gload = [&](int n0) {
 #pragma unroll
-    for (int c = 0; c < C::KCH; ++c) {
-      const int idx = tid + 256 * c;
+    for (int cc = 0; cc < C::KCH; ++cc) {
+      const int idx = tid + 256 * cc;
       const int row = idx / (D / 8), c8 = idx % (D / 8);
-      const int key = n0 + row;
-      kreg[c] = load16(kb + (int64_t)key * p.ks2 + 8 * c8, key < p.Lk);
+      const int key = min(n0 + row, last_key);  // rows past the end are masked as scores
+      kreg[cc] = load16_clamped(kb + (int64_t)key * p.ks2 + 8 * c8);
     }
 #pragma unroll
     for (int gg = 0; gg < C::VG; ++gg) {
-      const int gi = tid + 256 * gg;
+      const int gi = min(tid + 256 * gg, C::VGR - 1);
       const int p4 = gi / (D / 8), qd = gi % (D / 8);
+      uint32_t okm = 0;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = n0 + 4 * p4 + r;
-        vreg[gg][r] = load16(vb + (int64_t)key * p.vs2 + 8 * qd, gi < C::VGR && key < p.Lk);
+        okm |= (key < p.Lk ? 1u : 0u) << r;
+        vreg[gg][r] = load16_clamped(vb + (int64_t)min(key, last_key) * p.vs2 + 8 * qd);
       }
+      vok[gg] = okm;
     }
   };
   auto sstore = [&](uint16_t* buf) {
 #pragma unroll
-    for (int c = 0; c < C::KCH; ++c) {
-      const int idx = tid + 256 * c;
+    for (int cc = 0; cc < C::KCH; ++cc) {
+      const int idx = tid + 256 * cc;
       const int row = idx / (D / 8), c8 = idx % (D / 8);
-      *reinterpret_cast<u32x4*>(buf + row * C::KSTR + 8 * c8) = kreg[c];
+      *reinterpret_cast<u32x4*>(buf + row * C::KSTR + 8 * c8) = kreg[cc];
     }
     uint16_t* vt = buf + C::KBUF;
 #pragma unroll
     for (int gg = 0; gg < C::VG; ++gg) {
       const int gi = tid + 256 * gg;
-      if (gi < C::VGR) {
+      if (C::VGR % 256 == 0 || gi < C::VGR) {
         const int p4 = gi / (D / 8), qd = gi % (D / 8);
+        u32x4 r0 = zero_unless(vreg[gg][0], vok[gg] & 1u);
+        u32x4 r1 = zero_unless(vreg[gg][1], vok[gg] & 2u);
+        u32x4 r2 = zero_unless(vreg[gg][2], vok[gg] & 4u);
+        u32x4 r3 = zero_unless(vreg[gg][3], vok[gg] & 8u);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const int d = 8 * qd + 2 * w;
-          *reinterpret_cast<u32x2*>(vt + d * C::VSTR + 4 * p4) =
-              col4_even(vreg[gg][0][w], vreg[gg][1][w], vreg[gg][2][w], vreg[gg][3][w]);
-          *reinterpret_cast<u32x2*>(vt + (d + 1) * C::VSTR + 4 * p4) =
-              col4_odd(vreg[gg][0][w], vreg[gg][1][w], vreg[gg][2][w], vreg[gg][3][w]);
+          *reinterpret_cast<u32x2*>(vt + d * C::VSTR + 4 * p4) = col4_even(r0[w], r1[w], r2[w], r3[w]);
+          *reinterpret_cast<u32x2*>(vt + (d + 1) * C::VSTR + 4 * p4) = col4_odd(r0[w], r1[w], r2[w], r3[w]);
         }
       }
     }
@@ -153,37 +172,41 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
     if (n0 < wave_kend) {
       f32x16 s[C::MT];
 #pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) {
-        s[mt2] = f32x16{};
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < C::KK; ++kk) {
+      for (int kk = 0; kk < C::KK; ++kk) {
+#pragma unroll
+        for (int mt2 = 0; mt2 < C::MT; ++mt2) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (32 * mt2 + l32) * C::KSTR + 16 * kk + 8 * hl);
           s[mt2] = E::mfma(a, qf[kk], s[mt2]);
         }
       }
-      const bool need_mask = (n0 + BN > p.Lk) || (p.causal && n0 + BN - 1 > wave_diag0);
+      // mask (tiles crossing the diagonal or the key tail only) and row max
       float mx = -INFINITY;
+      if (n0 + BN - 1 > wave_lim0) {
 #pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) {
+        for (int mt2 = 0; mt2 < C::MT; ++mt2)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float x = s[mt2][e] * p.scale_log2;
-          if (need_mask) {
+          for (int e = 0; e < 16; ++e) {
             const int key = n0 + 32 * mt2 + 8 * (e >> 2) + 4 * hl + (e & 3);
-            const bool ok = key < p.Lk && (!p.causal || key <= diag);
-            x = ok ? x : -INFINITY;
+            s[mt2][e] = key <= lim ? s[mt2][e] : -INFINITY;
           }
-          s[mt2][e] = x;
-          mx = fmaxf(mx, x);
-        }
       }
-      mx = xhalf_max(mx);
-      const float m_new = fmaxf(m, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2_fast(m - m_use);
-      l *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+      for (int mt2 = 0; mt2 < C::MT; ++mt2)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt2][e]);
+      const float mxs = xhalf_max(mx) * c;
+      const bool grow = mxs > m + kLazyRescale;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float m_new = grow ? mxs : m;
+        const float alpha = grow ? exp2_fast(m - m_new) : 1.f;  // 0 when m was -inf
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+        m = m_new;
+      }
+      const float neg_m = m == -INFINITY ? 0.f : -m;
 
       u32x4 pb[2 * C::MT];
 #pragma unroll
@@ -193,8 +216,8 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const int e0 = 8 * cc + 2 * w;
-            const float p0 = exp2_fast(s[mt2][e0] - m_use);
-            const float p1 = exp2_fast(s[mt2][e0 + 1] - m_use);
+            const float p0 = exp2_fast(fmaf(s[mt2][e0], c, neg_m));
+            const float p1 = exp2_fast(fmaf(s[mt2][e0 + 1], c, neg_m));
             l += p0 + p1;
             pb[2 * mt2 + cc][w] = E::pack2(p0, p1);
           }
@@ -204,17 +227,16 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
       for (int dt = 0; dt < C::DT; ++dt) {
         const int drow = 32 * dt + l32;
 #pragma unroll
-        for (int c = 0; c < 2 * C::MT; ++c) {
+        for (int cc = 0; cc < 2 * C::MT; ++cc) {
           u32x4 a = {0u, 0u, 0u, 0u};
           if (D >= 32 || drow < D) {
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(vt + drow * C::VSTR + 16 * c + 4 * hl);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(vt + drow * C::VSTR + 16 * c + 8 + 4 * hl);
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(vt + drow * C::VSTR + 16 * cc + 4 * hl);
+            const u32x2 hi = *reinterpret_cast<const u32x2*>(vt + drow * C::VSTR + 16 * cc + 8 + 4 * hl);
             a = u32x4{lo[0], lo[1], hi[0], hi[1]};
           }
-          acc[dt] = E::mfma(a, pb[c], acc[dt]);
+          acc[dt] = E::mfma(a, pb[cc], acc[dt]);
         }
       }
-      m = m_new;
     }
 
     if (t + 1 < n_tiles) sstore(smem + ((t + 1) & 1) * C::BUF);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace cie {
@@ -21,7 +23,8 @@ struct FlashParams {
   int B, Hq, Hk, Lq, Lk, group;
   int n_mt;  // query tiles of 128 rows
   int n_wg;  // B * Hq * n_mt
-  float scale_log2;
+  float scale_log2;  // |scale| * log2(e), never below 1e-30
+  uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
   int causal;
 };
 
@@ -42,16 +45,19 @@ struct PagedParams {
   int B, Hq, Hk, Lq, group, R;  // R = group * Lq query rows per kv head
   int num_blocks, max_blocks, block_size;
   FastDiv bsdiv;
-  int split_len, n_splits;
-  float scale_log2;
+  int split_len, n_splits, n_qt;
+  float scale_log2;  // |scale| * log2(e), never below 1e-30
+  uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
   int causal;
 };
 
 constexpr int kPagedWaves = 4;
-constexpr int kPagedTile = 32;  // keys per wave iteration
+constexpr int kPagedTile = 32;             // keys per wave iteration
+constexpr int kPagedMaxSplitBlocks = 1024;  // block ids of one split staged in LDS
+constexpr int kPagedReduceChunk = 256;      // split weights staged per reduction step
 
 // Split length (multiple of kPagedWaves * kPagedTile) for a paged launch.
-int paged_split_len(int B, int Hk, int n_qt, int max_ctx);
+int paged_split_len(int B, int Hk, int n_qt, int max_ctx, int block_size);
 
 hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_paged(const PagedParams& p, int dtype, int D, hipStream_t stream);
