@@ -32,6 +32,8 @@ COMMON = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the online-softmax rescale multiplies them on the VALU
+    "-Xarch_device", "-mllvm=-amdgpu-mfma-vgpr-form=1",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

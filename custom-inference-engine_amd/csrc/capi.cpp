@@ -219,6 +219,18 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   p.max_blocks = max_blocks_per_seq;
   p.block_size = block_size;
   p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
+  {
+    // Largest element offset of either pool relative to its kv-head base.
+    const int64_t ext_k = (int64_t)(num_blocks > 0 ? num_blocks - 1 : 0) * kc_stride[0] +
+                          (int64_t)(block_size - 1) * kc_stride[1] + (int64_t)D;
+    const int64_t ext_v = (int64_t)(num_blocks > 0 ? num_blocks - 1 : 0) * vc_stride[0] +
+                          (int64_t)(block_size - 1) * vc_stride[1] + (int64_t)D;
+    const int64_t lim24 = (int64_t)1 << 24;
+    p.narrow = ext_k < ((int64_t)1 << 31) && ext_v < ((int64_t)1 << 31) && num_blocks < lim24 &&
+               kc_stride[0] < lim24 && kc_stride[1] < lim24 && vc_stride[0] < lim24 && vc_stride[1] < lim24;
+    p.ks0_24 = (uint32_t)kc_stride[0]; p.ks1_24 = (uint32_t)kc_stride[1];
+    p.vs0_24 = (uint32_t)vc_stride[0]; p.vs1_24 = (uint32_t)vc_stride[1];
+  }
   p.split_len = split_len;
   p.n_splits = n_splits;
   p.n_qt = n_qt;

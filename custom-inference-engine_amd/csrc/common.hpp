@@ -67,6 +67,23 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Balanced reductions over the 16 accumulator values of a lane (the compiler
+// does not reassociate a linear fmaxf / fadd chain).
+__device__ __forceinline__ float max16(const f32x16& v) {
+  float a0 = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  float a1 = fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7]));
+  float a2 = fmaxf(fmaxf(v[8], v[9]), fmaxf(v[10], v[11]));
+  float a3 = fmaxf(fmaxf(v[12], v[13]), fmaxf(v[14], v[15]));
+  return fmaxf(fmaxf(a0, a1), fmaxf(a2, a3));
+}
+__device__ __forceinline__ float sum16(const f32x16& v) {
+  float a0 = (v[0] + v[1]) + (v[2] + v[3]);
+  float a1 = (v[4] + v[5]) + (v[6] + v[7]);
+  float a2 = (v[8] + v[9]) + (v[10] + v[11]);
+  float a3 = (v[12] + v[13]) + (v[14] + v[15]);
+  return (a0 + a1) + (a2 + a3);
+}
+
 // Online-softmax weight of a partial whose running max is m against the new
 // max M: 0 for an empty partial (m = -inf), exp2(m - M) otherwise.
 __device__ __forceinline__ float rescale_weight(float m, float M) {
@@ -115,6 +132,49 @@ __device__ __forceinline__ u32x4 load16_stream(const uint16_t* p) {
 __device__ __forceinline__ u32x4 zero_unless(u32x4 v, bool ok) {
   return u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
 }
+
+// ---- LDS DMA and LDS transpose reads (gfx950) ------------------------------
+//
+// global_load_lds (16 bytes): lane l's 16 bytes land at lds_base + 16 * l,
+// lds_base wave-uniform (passed in M0). The load is issued from inline
+// assembly so that the compiler's wait-count pass does not treat it as an LDS
+// store aliasing every later LDS read (it would drain the whole queue with
+// vmcnt(0) before each one). Every consumer therefore waits explicitly with
+// vm_wait<N>(): N = number of vector-memory instructions issued after the
+// ones being waited for (they complete in order). M0 is written right before
+// each load; the kernels use no other M0-dependent instruction.
+//
+// ds_read_b64_tr_b16: within each 16-lane group, lane r supplies the address
+// of a row of four 16-bit elements M[r][0..3]; lane i receives
+// M[4j + i/4][i%4] for j = 0..3. With lane r pointing at
+// X[k0 + r/4][d0 + 4*(r%4)] of a row-major X[key][d], lane i receives
+// X[k0 .. k0+3][d0 + i]: four consecutive keys of one column, i.e. the
+// key-contiguous MFMA operand of X^T, read from row-major X.
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* gptr, void* lds_wave_base) {
+  const uint32_t lds_addr = (uint32_t)(size_t)(lds_void*)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* lds_ptr) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)lds_ptr);
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// Explicit waits are inline assembly so no compiler pass can relax them.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void lgkm_wait0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Transpose helpers for 16-bit data held two per dword: from four rows
 // r0..r3 (dword w covers columns 2w, 2w+1) build the 4 keys of column 2w

@@ -44,6 +44,8 @@ struct PagedParams {
   int64_t os0, os1, os2;
   int B, Hq, Hk, Lq, group, R;  // R = group * Lq query rows per kv head
   int num_blocks, max_blocks, block_size;
+  int narrow;  // every pool element offset < 2^31, ids and block/offset strides < 2^24
+  uint32_t ks0_24, ks1_24, vs0_24, vs1_24;
   FastDiv bsdiv;
   int split_len, n_splits, n_qt;
   float scale_log2;  // |scale| * log2(e), never below 1e-30
@@ -53,7 +55,7 @@ struct PagedParams {
 
 constexpr int kPagedWaves = 4;
 constexpr int kPagedTile = 32;             // keys per wave iteration
-constexpr int kPagedMaxSplitBlocks = 1024;  // block ids of one split staged in LDS
+constexpr int kPagedMaxSplitBlocks = 528;  // block ids of one split staged in LDS
 constexpr int kPagedReduceChunk = 256;      // split weights staged per reduction step
 
 // Split length (multiple of kPagedWaves * kPagedTile) for a paged launch.

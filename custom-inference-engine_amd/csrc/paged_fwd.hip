@@ -4,24 +4,26 @@
 // (engine/model/block.py:56-71: cache.gather -> index_select of the whole
 // history, engine/cache/kv_cache.py:141-165, then the dense Triton kernel):
 // K and V are read once, straight out of the (num_blocks, block_size, Hk, D)
-// pool through the int32 block table, with 16-byte loads.
+// pool through the int32 block table.
 //
-// One workgroup (4 waves) per (sequence, context split, query tile, kv head);
-// the kv heads of one (sequence, split) are adjacent workgroup ids so the
-// pool blocks they share (block_size * Hk * D contiguous elements) are read
-// at the same time. All Hq/Hk query heads x Lq new tokens of a kv head
-// (R = group * Lq rows, up to 32 per query tile) share each K/V byte. The
-// split's block ids are staged in LDS once; each wave then walks every 4th
-// 32-key tile of the split:
-//   S^T[32 x 32] = K_tile . Q^T    K rows go from global memory straight into
-//                                   the MFMA A operand (one token row per lane)
+// One wave per (sequence, context split, query tile, kv head). The kv heads
+// of one (sequence, split) are adjacent workgroup ids, so the pool blocks they
+// share (block_size * Hk * D contiguous elements) are read at the same time.
+// All Hq/Hk query heads x Lq new tokens of a kv head (R = group * Lq rows, up
+// to 32 per query tile) share each K/V byte.
+//
+// Memory path: the split's block ids are staged in LDS; K and V tiles of 32
+// tokens are copied global -> LDS by 16-byte direct-to-LDS loads into a ring
+// of NST stages (NST-1 tiles in flight, no VGPR staging). Rows are stored
+// with their 16-byte chunks XOR-swizzled by (token & 7) so the fragment reads
+// below are conflict-free.
+// Per tile:
+//   S^T[32 x 32] = K_tile . Q^T    A operand: ds_read_b128 of one token row
 //   online softmax in registers (one v_permlane32_swap per reduction)
-//   O^T += V^T_tile . P^T          V tile transposed through a per-wave LDS slab
-// Loads are unconditional (addresses clamped to a valid token, data of
-// out-of-range tokens zeroed or masked), so a tile's loads stay in flight
-// together. The 4 waves merge in LDS; a workgroup whose sequence has a single
-// split writes the final output, otherwise it writes (m, l, acc) partials
-// that paged_reduce_kernel combines.
+//   O^T += V^T_tile . P^T          A operand: ds_read_b64_tr_b16 turns the
+//                                   row-major V tile into key-contiguous V^T
+// A wave whose sequence has a single split writes the final output; otherwise
+// it writes (m, l, acc) partials that paged_reduce_kernel combines.
 #include "kernels.hpp"
 
 namespace cie {
@@ -32,22 +34,29 @@ template <int D>
 struct PagedCfg {
   static constexpr int KK = D / 16;
   static constexpr int DT = D >= 32 ? D / 32 : 1;
-  static constexpr int VSTR = kPagedTile + 4;           // LDS pitch of a V^T row (elements)
-  static constexpr int VT_WAVE = D * VSTR;              // elements per wave slab
-  static constexpr int VGL = (D + 63) / 64;             // 4-token x 8-dim V groups per lane
-  static constexpr int MERGE = DT * 16 * 64 + 2 * 64;   // floats per merge slot
-  static constexpr int LDS_VT = kPagedWaves * VT_WAVE * 2;
-  static constexpr int LDS_MERGE = 2 * MERGE * 4;
-  static constexpr int LDS_WORK = LDS_VT > LDS_MERGE ? LDS_VT : LDS_MERGE;
-  static constexpr int LDS = LDS_WORK + kPagedMaxSplitBlocks * 4;  // + staged block ids
+  static constexpr int S = D / 8;                         // 16-byte chunks per token row
+  static constexpr int SWZ = (S < 8 ? S : 8) - 1;         // row swizzle mask
+  static constexpr int NDMA = S / 2;                      // 1 KiB loads per tensor per tile
+  static constexpr int NST = D <= 64 ? 3 : 2;
+  static constexpr int TILE = kPagedTile * D;             // elements of one tensor tile
+  static constexpr int STAGE = 2 * TILE;                  // K tile, then V tile
 };
 
+template <int N, int NDMA>
+__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  // vmcnt counts the 2 * NDMA loads of every tile issued after the one needed
+  if (N > 3 && ahead >= 3) vm_wait<(N > 3 ? 3 : 0) * 2 * NDMA>();
+  else if (N > 2 && ahead == 2) vm_wait<(N > 2 ? 2 : 0) * 2 * NDMA>();
+  else if (N > 1 && ahead == 1) vm_wait<2 * NDMA>();
+  else vm_wait<0>();
+}
+
 template <int DTYPE, int D>
-__global__ __launch_bounds__(256) void paged_fwd_kernel(const PagedParams p) {
+__global__ __launch_bounds__(64) void paged_fwd_kernel(const PagedParams p) {
   using C = PagedCfg<D>;
   using E = Elt<DTYPE>;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[C::LDS];
-  int32_t* sbt = reinterpret_cast<int32_t*>(smem + C::LDS_WORK);
+  __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
+  __shared__ int32_t sbt[kPagedMaxSplitBlocks];
 
   // blockIdx.x = ((b * n_splits + s) * n_qt + qt) * Hk + kvh
   int id = blockIdx.x;
@@ -57,30 +66,17 @@ __global__ __launch_bounds__(256) void paged_fwd_kernel(const PagedParams p) {
   id /= p.n_qt;
   const int s = id % p.n_splits;
   const int b = id / p.n_splits;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hl = lane >> 5;
+  const int lane = threadIdx.x, l32 = lane & 31, hl = lane >> 5;
 
   int ctx = p.lens[b];
   const bool bad_len = ctx < 0 || ctx > p.max_blocks * p.block_size || ctx > p.n_splits * p.split_len ||
                        (ctx > 0 && p.num_blocks < 1);
   if (bad_len) ctx = 0;  // never dereference; the output is poisoned below
   const int nsb = max(1, (ctx + p.split_len - 1) / p.split_len);
-  if (s >= nsb) return;  // uniform over the workgroup
+  if (s >= nsb) return;
   const int split0 = s * p.split_len;
   const int split1 = min(ctx, split0 + p.split_len);
-
-  // Stage the split's block ids (validated) in LDS.
-  const int blk0 = split1 > split0 ? (int)fdiv((uint32_t)split0, p.bsdiv) : 0;
-  const int nblk = split1 > split0 ? (int)fdiv((uint32_t)(split1 - 1), p.bsdiv) - blk0 + 1 : 0;
-  bool bad_blk = false;
-  const int32_t* btr = p.bt + (int64_t)b * p.max_blocks;
-  for (int j = tid; j < nblk; j += 256) {
-    const int bid = btr[blk0 + j];
-    const bool inb = bid >= 0 && bid < p.num_blocks;
-    bad_blk |= !inb;
-    sbt[j] = inb ? bid : 0;
-  }
-  const bool any_bad = __syncthreads_or(bad_blk ? 1 : 0) != 0;
+  const int ntiles = split1 > split0 ? (split1 - split0 + kPagedTile - 1) / kPagedTile : 0;
 
   // Query row of this lane: r = g * Lq + i (query head kvh*group + g, token i).
   const int r = qt * 32 + l32;
@@ -95,41 +91,71 @@ __global__ __launch_bounds__(256) void paged_fwd_kernel(const PagedParams p) {
     qf[kk] = load16(qrow + 16 * kk + 8 * hl, rv);
     qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
   }
+
+  // Stage the split's block ids (validated) in LDS.
+  const int blk0 = ntiles ? (int)fdiv((uint32_t)split0, p.bsdiv) : 0;
+  const int nblk = ntiles ? (int)fdiv((uint32_t)(split1 - 1), p.bsdiv) - blk0 + 1 : 0;
+  bool bad_blk = false;
+  const int32_t* btr = p.bt + (int64_t)b * p.max_blocks;
+  for (int j = lane; j < nblk; j += 64) {
+    const int bid = btr[blk0 + j];
+    const bool inb = bid >= 0 && bid < p.num_blocks;
+    bad_blk |= !inb;
+    sbt[j] = inb ? bid : 0;
+  }
+  const bool any_bad = __builtin_amdgcn_ballot_w64(bad_blk) != 0;
+  // Q and the block ids are in registers / LDS before the first LDS DMA is
+  // issued; an explicit wait here keeps the compiler from draining the DMA
+  // queue inside the tile loop on their account.
+  vm_wait<0>();
+
   // Last key visible to this row: the Lq new tokens are the newest Lq
-  // positions of the context (bottom-right causal alignment).
+  // positions of the context (bottom-right causal alignment). lim_min is the
+  // smallest lim of the wave; tiles entirely at or below it need no mask.
   const int lim = min(split1 - 1, p.causal ? ctx - p.Lq + i : ctx - 1);
+  const int lim_min = min(split1 - 1, p.causal ? ctx - p.Lq : ctx - 1);
   const float c = p.scale_log2;
 
   const uint16_t* kbase = p.kc + kvh * p.ks2;
   const uint16_t* vbase = p.vc + kvh * p.vs2;
   const int last = split1 - 1;
-  // Pool row of token t, clamped into this split (valid whenever the split is non-empty).
-  auto row_ptr = [&](const uint16_t* base, int64_t s0, int64_t s1, int t) -> const uint16_t* {
-    t = min(t, last);
-    const uint32_t blk = fdiv((uint32_t)t, p.bsdiv);
-    const uint32_t off = (uint32_t)t - blk * (uint32_t)p.block_size;
-    return base + (int64_t)sbt[blk - blk0] * s0 + (int64_t)off * s1;
-  };
 
-  u32x4 kn[C::KK];
-  u32x4 vn[C::VGL][4];
-  uint32_t vok[C::VGL];
-  auto gload = [&](int t0) {
-    const uint16_t* kp = row_ptr(kbase, p.ks0, p.ks1, t0 + l32);
+  // Tile copy: load j of a tile moves 16-byte chunk P = 64 j + lane, i.e.
+  // chunk (P % S) XOR swizzle of token P / S. Per-lane parts are fixed.
+  int ltok[C::NDMA], lchk[C::NDMA];
 #pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk) kn[kk] = load16_stream(kp + 16 * kk + 8 * hl);
+  for (int j = 0; j < C::NDMA; ++j) {
+    const int P = 64 * j + lane;
+    ltok[j] = P / C::S;
+    lchk[j] = 8 * ((P % C::S) ^ (ltok[j] & C::SWZ));
+  }
+  // Copy tile k (tokens split0 + 32k ...) into ring stage k % NST. Tokens past
+  // the split are clamped to its last token (masked as scores, zero weight).
+  auto issue = [&](int k) {
+    const int t0 = split0 + kPagedTile * k;
+    uint16_t* st = ring + (k % C::NST) * C::STAGE;
+    int bid[C::NDMA], off[C::NDMA];
 #pragma unroll
-    for (int gg = 0; gg < C::VGL; ++gg) {
-      const int gi = min(lane + 64 * gg, D - 1);
-      const int p4 = gi / (D / 8), qd = gi % (D / 8);
-      uint32_t okm = 0;
+    for (int j = 0; j < C::NDMA; ++j) {  // all block-id reads in flight together
+      const int t = min(t0 + ltok[j], last);
+      const uint32_t blk = fdiv((uint32_t)t, p.bsdiv);
+      off[j] = t - (int)blk * p.block_size;
+      bid[j] = sbt[blk - blk0];
+    }
+    if (p.narrow) {  // pool offsets < 2^31 elements, ids and strides < 2^24: 24-bit multiplies
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int t = t0 + 4 * p4 + rr;
-        okm |= (t < split1 ? 1u : 0u) << rr;
-        vn[gg][rr] = load16_stream(row_ptr(vbase, p.vs0, p.vs1, t) + 8 * qd);
+      for (int j = 0; j < C::NDMA; ++j) {
+        const uint32_t ko = __umul24(bid[j], p.ks0_24) + __umul24(off[j], p.ks1_24) + lchk[j];
+        const uint32_t vo = __umul24(bid[j], p.vs0_24) + __umul24(off[j], p.vs1_24) + lchk[j];
+        dma16(kbase + ko, st + 512 * j);
+        dma16(vbase + vo, st + C::TILE + 512 * j);
       }
-      vok[gg] = okm;
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::NDMA; ++j) {
+        dma16(kbase + (int64_t)bid[j] * p.ks0 + (int64_t)off[j] * p.ks1 + lchk[j], st + 512 * j);
+        dma16(vbase + (int64_t)bid[j] * p.vs0 + (int64_t)off[j] * p.vs1 + lchk[j], st + C::TILE + 512 * j);
+      }
     }
   };
 
@@ -138,35 +164,34 @@ __global__ __launch_bounds__(256) void paged_fwd_kernel(const PagedParams p) {
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
   float m = -INFINITY, l = 0.f;
 
-  uint16_t* vtw = reinterpret_cast<uint16_t*>(smem) + wave * C::VT_WAVE;
-  constexpr int kStep = kPagedWaves * kPagedTile;
-  int t0 = split0 + kPagedTile * wave;
-  if (t0 < split1) gload(t0);
-  for (; t0 < split1; t0 += kStep) {
-    u32x4 kc[C::KK];
-    u32x4 vc[C::VGL][4];
-    uint32_t vokc[C::VGL];
-#pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk) kc[kk] = kn[kk];
-#pragma unroll
-    for (int gg = 0; gg < C::VGL; ++gg) {
-      vokc[gg] = vok[gg];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) vc[gg][rr] = vn[gg][rr];
+  const int pro = min(C::NST - 1, ntiles);
+  for (int k = 0; k < pro; ++k) issue(k);
+  for (int n = 0; n < ntiles; ++n) {
+    if (n + C::NST - 1 < ntiles) {
+      lgkm_wait0();  // the previous tile's LDS reads of the recycled stage are done
+      issue(n + C::NST - 1);
     }
-    if (t0 + kStep < split1) gload(t0 + kStep);
+    wait_tiles_ahead<C::NST, C::NDMA>(min(C::NST - 1, ntiles - 1 - n));
+    const uint16_t* kst = ring + (n % C::NST) * C::STAGE;
+    const uint16_t* vst = kst + C::TILE;
+    const int t0 = split0 + kPagedTile * n;
 
     f32x16 sc = f32x16{};
 #pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk) sc = E::mfma(kc[kk], qf[kk], sc);
-
-    float mx = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int key = t0 + 8 * (e >> 2) + 4 * hl + (e & 3);
-      sc[e] = key <= lim ? sc[e] : -INFINITY;
-      mx = fmaxf(mx, sc[e]);
+    for (int kk = 0; kk < C::KK; ++kk) {
+      const int slot = (2 * kk + hl) ^ (l32 & C::SWZ);
+      const u32x4 a = *reinterpret_cast<const u32x4*>(kst + (l32 * C::S + slot) * 8);
+      sc = E::mfma(a, qf[kk], sc);
     }
+
+    if (t0 + kPagedTile - 1 > lim_min) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = t0 + 8 * (e >> 2) + 4 * hl + (e & 3);
+        sc[e] = key <= lim ? sc[e] : -INFINITY;
+      }
+    }
+    const float mx = max16(sc);
     const float mxs = xhalf_max(mx) * c;
     const bool grow = mxs > m + kLazyRescalePaged;
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -178,90 +203,34 @@ __global__ __launch_bounds__(256) void paged_fwd_kernel(const PagedParams p) {
       m = m_new;
     }
     const float neg_m = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = exp2_fast(fmaf(sc[e], c, neg_m));
+    l += sum16(sc);
     u32x4 pb[2];
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
+    for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int e0 = 8 * cc + 2 * w;
-        const float p0 = exp2_fast(fmaf(sc[e0], c, neg_m));
-        const float p1 = exp2_fast(fmaf(sc[e0 + 1], c, neg_m));
-        l += p0 + p1;
-        pb[cc][w] = E::pack2(p0, p1);
-      }
-    }
+      for (int w = 0; w < 4; ++w) pb[cc][w] = E::pack2(sc[8 * cc + 2 * w], sc[8 * cc + 2 * w + 1]);
 
-    // V tile -> V^T slab of this wave (LDS ops of one wave complete in order).
-#pragma unroll
-    for (int gg = 0; gg < C::VGL; ++gg) {
-      const int gi = lane + 64 * gg;
-      if (D % 64 == 0 || gi < D) {
-        const int p4 = gi / (D / 8), qd = gi % (D / 8);
-        const u32x4 r0 = zero_unless(vc[gg][0], vokc[gg] & 1u);
-        const u32x4 r1 = zero_unless(vc[gg][1], vokc[gg] & 2u);
-        const u32x4 r2 = zero_unless(vc[gg][2], vokc[gg] & 4u);
-        const u32x4 r3 = zero_unless(vc[gg][3], vokc[gg] & 8u);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int d = 8 * qd + 2 * w;
-          *reinterpret_cast<u32x2*>(vtw + d * C::VSTR + 4 * p4) = col4_even(r0[w], r1[w], r2[w], r3[w]);
-          *reinterpret_cast<u32x2*>(vtw + (d + 1) * C::VSTR + 4 * p4) = col4_odd(r0[w], r1[w], r2[w], r3[w]);
-        }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // V^T fragments: lane (group gq = lane/16, r = lane%16) points at token
+    // k0 + r/4, dims d0 + 4*(r%4); the transpose read hands lane l the four
+    // keys k0..k0+3 of dim 32*dt + lane%32.
+    const int rq = lane & 15, gq = lane >> 4;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
-      const int drow = 32 * dt + l32;
+      int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
+      if (D < 32) d = min(d, D - 4);  // rows >= D of O^T are discarded
+      const int chunk = d >> 3, within = d & 7;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
-        u32x4 a = {0u, 0u, 0u, 0u};
-        if (D >= 32 || drow < D) {
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vtw + drow * C::VSTR + 16 * cc + 4 * hl);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vtw + drow * C::VSTR + 16 * cc + 8 + 4 * hl);
-          a = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
-        acc[dt] = E::mfma(a, pb[cc], acc[dt]);
+        const int tlo = 16 * cc + 4 * hl + (rq >> 2);
+        const int thi = tlo + 8;
+        const u32x2 lo = lds_read_tr16(vst + (tlo * C::S + (chunk ^ (tlo & C::SWZ))) * 8 + within);
+        const u32x2 hi = lds_read_tr16(vst + (thi * C::S + (chunk ^ (thi & C::SWZ))) * 8 + within);
+        acc[dt] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[cc], acc[dt]);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-
-  // Merge the 4 waves' partial softmax states: (1,3) into (0,2), then 2 into 0.
-  float* mb = reinterpret_cast<float*>(smem);
-  auto put = [&](float* slot) {
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) slot[(dt * 16 + e) * 64 + lane] = acc[dt][e];
-    slot[C::DT * 16 * 64 + lane] = m;
-    slot[C::DT * 16 * 64 + 64 + lane] = l;
-  };
-  auto take = [&](const float* slot) {
-    const float mo = slot[C::DT * 16 * 64 + lane];
-    const float lo = slot[C::DT * 16 * 64 + 64 + lane];
-    const float M = fmaxf(m, mo);
-    const float wa = rescale_weight(m, M), wb = rescale_weight(mo, M);
-    l = l * wa + lo * wb;
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[dt][e] = acc[dt][e] * wa + slot[(dt * 16 + e) * 64 + lane] * wb;
-    m = M;
-  };
-  __syncthreads();
-  if (wave & 1) put(mb + (wave >> 1) * C::MERGE);
-  __syncthreads();
-  if (!(wave & 1)) take(mb + (wave >> 1) * C::MERGE);
-  __syncthreads();
-  if (wave == 2) put(mb);
-  __syncthreads();
-  if (wave != 0) return;
-  take(mb);
 
   const float l_tot = xhalf_sum(l);
   if (!rv) return;
@@ -369,20 +338,19 @@ __global__ __launch_bounds__(64) void paged_reduce_kernel(const PagedParams p) {
 }
 
 int paged_split_len(int B, int Hk, int n_qt, int max_ctx, int block_size) {
-  constexpr int kStep = kPagedWaves * kPagedTile;
-  // The split's block ids must fit the LDS staging area.
-  const int64_t cap_tokens = (int64_t)(kPagedMaxSplitBlocks - 2) * block_size;
-  const int cap = (int)std::min<int64_t>(1 << 20, std::max<int64_t>(kStep, cap_tokens / kStep * kStep));
+  // Longest split (<= 512 tokens) that still yields about 1.5k waves at the
+  // longest context; the split's block ids must fit the LDS staging area.
   const int64_t pairs = (int64_t)B * Hk * n_qt;
-  int split = std::min(2 * kStep, cap);
-  while (split < max_ctx && 2 * split <= cap && pairs * ((max_ctx + split - 1) / split) > 2048) split *= 2;
+  const int64_t cap = std::max<int64_t>(kPagedTile, (int64_t)(kPagedMaxSplitBlocks - 2) * block_size);
+  int split = 512;
+  while (split > kPagedTile && (split > cap || pairs * ((max_ctx + split - 1) / split) < 1536)) split /= 2;
   return split;
 }
 
 template <int DTYPE, int D>
 static hipError_t launch_paged_t(const PagedParams& p, hipStream_t stream) {
   const int64_t n_wg = (int64_t)p.B * p.n_splits * p.n_qt * p.Hk;
-  hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D>), dim3((unsigned)n_wg), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D>), dim3((unsigned)n_wg), dim3(64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.n_splits <= 1) return e;
   hipLaunchKernelGGL((paged_reduce_kernel<DTYPE, D>), dim3(p.B * p.Hq * p.Lq), dim3(64), 0, stream, p);

@@ -116,8 +116,8 @@ def test_paged_rejects_bad_arguments(over, code):
 
 def test_paged_workspace_size():
     lib = _lib.load()
-    # one split -> no workspace
-    assert lib.cie_paged_workspace_bytes(4, 32, 8, 1, 64, 200, 16, 13) == 0
+    # contexts within one 32-token tile never split -> no workspace
+    assert lib.cie_paged_workspace_bytes(4, 32, 8, 1, 64, 32, 16, 2) == 0
     # long contexts split: B*Hq*Lq*n_splits*(D+2)*4 bytes
     n = lib.cie_paged_workspace_bytes(32, 32, 8, 1, 64, 4096, 16, 256)
     assert n > 0 and n % (32 * 32 * 1 * (64 + 2) * 4) == 0
