@@ -30,16 +30,22 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Element traits: 0 = fp16, 1 = bf16 (the CIE_DTYPE_* codes).
 template <int DTYPE> struct Elt;
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 template <> struct Elt<0> {
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
-  // Round-to-nearest-even conversion of two floats, packed low|high.
+  // Round-to-nearest-even conversion of two floats, packed low|high (v_cvt_pk_f16_f32).
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    _Float16 a = (_Float16)lo, b = (_Float16)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_f16 against ones).
+  static __device__ __forceinline__ float sum2(uint32_t pk, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk), f16x2{(_Float16)1.f, (_Float16)1.f}, acc, false);
   }
 };
 
@@ -49,16 +55,25 @@ template <> struct Elt<1> {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    __bf16 a = (__bf16)lo, b = (__bf16)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  }
+  static __device__ __forceinline__ float sum2(uint32_t pk, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), bf16x2{(__bf16)1.f, (__bf16)1.f}, acc,
+                                           false);
   }
 };
+
+// NaN-propagating maximum (llvm.maximum): selects to v_maximum3_f32 with no
+// quieting of the operands, which fmaxf needs in IEEE mode (a v_max_f32 x, x
+// per operand). NaN scores (from NaN inputs) propagate like the reference's
+// softmax.
+__device__ __forceinline__ float maxf(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max3f(float a, float b, float c) { return maxf(maxf(a, b), c); }
 
 // Reductions over the two lanes (l, l ^ 32) that share a query row.
 __device__ __forceinline__ float xhalf_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max3f(__uint_as_float(r[0]), __uint_as_float(r[1]), x);
 }
 __device__ __forceinline__ float xhalf_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -70,11 +85,9 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // Balanced reductions over the 16 accumulator values of a lane (the compiler
 // does not reassociate a linear fmaxf / fadd chain).
 __device__ __forceinline__ float max16(const f32x16& v) {
-  float a0 = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-  float a1 = fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7]));
-  float a2 = fmaxf(fmaxf(v[8], v[9]), fmaxf(v[10], v[11]));
-  float a3 = fmaxf(fmaxf(v[12], v[13]), fmaxf(v[14], v[15]));
-  return fmaxf(fmaxf(a0, a1), fmaxf(a2, a3));
+  const float a0 = max3f(v[0], v[1], v[2]), a1 = max3f(v[3], v[4], v[5]), a2 = max3f(v[6], v[7], v[8]);
+  const float a3 = max3f(v[9], v[10], v[11]), a4 = max3f(v[12], v[13], v[14]);
+  return max3f(max3f(a0, a1, a2), max3f(a3, a4, v[15]), a0);
 }
 __device__ __forceinline__ float sum16(const f32x16& v) {
   float a0 = (v[0] + v[1]) + (v[2] + v[3]);
@@ -157,7 +170,8 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* gptr, void* lds_wave_base) {
-  const uint32_t lds_addr = (uint32_t)(size_t)(lds_void*)lds_wave_base;
+  // lds_wave_base is uniform across the wave by contract; readfirstlane puts it in an SGPR
+  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_void*)lds_wave_base);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
 }
 #pragma clang diagnostic pop

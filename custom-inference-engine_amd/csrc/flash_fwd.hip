@@ -2,16 +2,22 @@
 //
 // Replaces the Triton program kernels/flash_attention.py:21-120 and the GQA
 // expansion of its wrapper (:150-155): a workgroup of 4 waves owns 128 query
-// rows of one query head (32 rows per wave), streams the K/V tiles of the kv
-// head h / (Hq / Hk) through double-buffered LDS, and keeps the online-softmax
-// state (running max m, row sum l, output accumulator) in registers.
+// rows of one query head (32 rows per wave) and streams the K/V tiles of kv
+// head h / (Hq / Hk) through an LDS ring; the online-softmax state (running
+// max m, row sum l, output accumulator) stays in registers.
 //
-// Per K/V tile of BN keys and per wave:
-//   S^T[BN x 32] = K_tile . Q_w^T        MFMA 32x32x16, K from LDS (row-major),
-//                                          Q^T resident in registers
+// Memory path: each K/V tile (BN keys) is copied global -> LDS by 16-byte
+// direct-to-LDS loads issued by all four waves (no VGPR staging), row-major
+// with the 16-byte chunks of row r XOR-swizzled by (r & 7). NST-1 tiles are in
+// flight while one is computed; one workgroup barrier per tile both publishes
+// the new tile and frees the stage that is refilled next.
+// Per tile and wave:
+//   S^T[BN x 32] = K_tile . Q_w^T     MFMA 32x32x16; A = ds_read_b128 of K rows,
+//                                      B = Q^T resident in registers
 //   mask + running max (one v_permlane32_swap), p = exp2(s*c - m), c = scale*log2e
-//   O^T[D x 32] += V^T_tile . P^T         MFMA 32x32x16, V^T from LDS, P^T
-//                                          straight from the S^T registers
+//   O^T[D x 32] += V^T_tile . P^T      MFMA 32x32x16; A = ds_read_b64_tr_b16 of
+//                                      the row-major V tile, B = P^T straight
+//                                      from the S^T registers
 // The bottom-right causal rule (key j visible to row i iff j <= Lk - Lq + i,
 // kernels/flash_attention.py:99-102) is applied only on tiles that cross a
 // wave's diagonal or the key tail; a workgroup stops at the last key any of
@@ -21,6 +27,7 @@
 // a tile raises the row max by more than 2^8 (so p <= 256, exact to fp16 /
 // bf16 rounding), and the accumulator rescale is skipped for the whole wave
 // when no row needs it. The final acc / l is unchanged by the choice of m.
+// l accumulates the probabilities as rounded for the P.V product.
 #include "kernels.hpp"
 
 namespace cie {
@@ -29,28 +36,33 @@ constexpr float kLazyRescale = 8.0f;  // log2 of the largest p tolerated before 
 
 template <int D>
 struct FlashCfg {
-  static constexpr int BM = 128;                                            // query rows per workgroup
-  static constexpr int BN = D <= 32 ? 128 : (D <= 128 ? 64 : 32);           // keys per tile
-  static constexpr int KSTR = D + 8;                                        // LDS row pitch of K
-  static constexpr int VSTR = BN + 4;                                       // LDS row pitch of V^T
-  static constexpr int DT = D >= 32 ? D / 32 : 1;                           // 32-row output tiles
-  static constexpr int KK = D / 16;                                         // MFMA steps over head_dim
-  static constexpr int MT = BN / 32;                                        // 32-key score tiles
-  static constexpr int KBUF = BN * KSTR;
-  static constexpr int VBUF = D * VSTR;
-  static constexpr int BUF = KBUF + VBUF;                                   // elements per LDS stage
-  static constexpr int KCH = BN * D / 8 / 256;                              // 16-byte K chunks per thread
-  static constexpr int VGR = (BN / 4) * (D / 8);                            // 4-key x 8-dim V groups
-  static constexpr int VG = (VGR + 255) / 256;                              // V groups per thread
-  static_assert(KCH >= 1 && BN * D / 8 == KCH * 256, "K tile must split evenly over 256 threads");
+  static constexpr int BM = 128;                                   // query rows per workgroup
+  static constexpr int BN = D <= 32 ? 128 : (D <= 128 ? 64 : 32);  // keys per tile
+  static constexpr int S = D / 8;                                  // 16-byte chunks per row
+  static constexpr int SWZ = (S < 8 ? S : 8) - 1;                  // row swizzle mask
+  static constexpr int DT = D >= 32 ? D / 32 : 1;                  // 32-row output tiles
+  static constexpr int KK = D / 16;                                // MFMA steps over head_dim
+  static constexpr int MT = BN / 32;                               // 32-key score tiles
+  static constexpr int TILE = BN * D;                              // elements of one tensor tile
+  static constexpr int STAGE = 2 * TILE;                           // K tile, then V tile
+  static constexpr int NST = D <= 64 ? 3 : 2;                      // ring stages
+  static constexpr int NW = BN * S / 256;                          // 1 KiB copies per wave per tensor
+  static constexpr int OCC = D <= 64 ? 3 : (D == 128 ? 2 : 1);     // workgroups per CU
+  static_assert(NW >= 1 && BN * S == NW * 256, "tile must split evenly over 4 waves");
 };
 
+template <int NST, int PER_TILE>
+__device__ __forceinline__ void wait_prefill_tile(int ahead) {
+  if (NST > 2 && ahead >= 1) vm_wait<(NST > 2 ? 1 : 0) * PER_TILE>();
+  else vm_wait<0>();
+}
+
 template <int DTYPE, int D>
-__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(const FlashParams p) {
+__global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const FlashParams p) {
   using C = FlashCfg<D>;
   using E = Elt<DTYPE>;
   constexpr int BN = C::BN;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * C::BUF];
+  __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
 
   // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous run of logical tiles so the query heads of a kv head (and its
@@ -100,152 +112,120 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(const FlashParams p) 
   const uint16_t* vb = p.v + b * p.vs0 + kvh * p.vs1;
   const int last_key = max(p.Lk - 1, 0);
 
-  u32x4 kreg[C::KCH];
-  u32x4 vreg[C::VG][4];
-  uint32_t vok[C::VG];  // bit r: key 4*p4 + r of the group exists
-  auto gload = [&](int n0) {
+  // Tile copy: copy j of this wave moves 16-byte chunk P = (wave*NW + j)*64 + lane
+  // of the tile, i.e. row P / S, chunk (P % S) XOR (row & 7). Rows past the
+  // last key are clamped to it (masked as scores, zero weight in P.V).
+  int lrow[C::NW], lchk[C::NW];
 #pragma unroll
-    for (int cc = 0; cc < C::KCH; ++cc) {
-      const int idx = tid + 256 * cc;
-      const int row = idx / (D / 8), c8 = idx % (D / 8);
-      const int key = min(n0 + row, last_key);  // rows past the end are masked as scores
-      kreg[cc] = load16_clamped(kb + (int64_t)key * p.ks2 + 8 * c8);
-    }
+  for (int j = 0; j < C::NW; ++j) {
+    const int P = (wave * C::NW + j) * 64 + lane;
+    lrow[j] = P / C::S;
+    lchk[j] = 8 * ((P % C::S) ^ (lrow[j] & C::SWZ));
+  }
+  auto issue = [&](int t) {
+    const int n0 = t * BN;
+    uint16_t* st = ring + (t % C::NST) * C::STAGE + wave * C::NW * 512;
 #pragma unroll
-    for (int gg = 0; gg < C::VG; ++gg) {
-      const int gi = min(tid + 256 * gg, C::VGR - 1);
-      const int p4 = gi / (D / 8), qd = gi % (D / 8);
-      uint32_t okm = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = n0 + 4 * p4 + r;
-        okm |= (key < p.Lk ? 1u : 0u) << r;
-        vreg[gg][r] = load16_clamped(vb + (int64_t)min(key, last_key) * p.vs2 + 8 * qd);
-      }
-      vok[gg] = okm;
-    }
-  };
-  auto sstore = [&](uint16_t* buf) {
-#pragma unroll
-    for (int cc = 0; cc < C::KCH; ++cc) {
-      const int idx = tid + 256 * cc;
-      const int row = idx / (D / 8), c8 = idx % (D / 8);
-      *reinterpret_cast<u32x4*>(buf + row * C::KSTR + 8 * c8) = kreg[cc];
-    }
-    uint16_t* vt = buf + C::KBUF;
-#pragma unroll
-    for (int gg = 0; gg < C::VG; ++gg) {
-      const int gi = tid + 256 * gg;
-      if (C::VGR % 256 == 0 || gi < C::VGR) {
-        const int p4 = gi / (D / 8), qd = gi % (D / 8);
-        u32x4 r0 = zero_unless(vreg[gg][0], vok[gg] & 1u);
-        u32x4 r1 = zero_unless(vreg[gg][1], vok[gg] & 2u);
-        u32x4 r2 = zero_unless(vreg[gg][2], vok[gg] & 4u);
-        u32x4 r3 = zero_unless(vreg[gg][3], vok[gg] & 8u);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int d = 8 * qd + 2 * w;
-          *reinterpret_cast<u32x2*>(vt + d * C::VSTR + 4 * p4) = col4_even(r0[w], r1[w], r2[w], r3[w]);
-          *reinterpret_cast<u32x2*>(vt + (d + 1) * C::VSTR + 4 * p4) = col4_odd(r0[w], r1[w], r2[w], r3[w]);
-        }
-      }
+    for (int j = 0; j < C::NW; ++j) {
+      const int key = min(n0 + lrow[j], last_key);
+      dma16(kb + (int64_t)key * p.ks2 + lchk[j], st + 512 * j);
+      dma16(vb + (int64_t)key * p.vs2 + lchk[j], st + C::TILE + 512 * j);
     }
   };
 
   f32x16 acc[C::DT];
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY, l = 0.f, l2 = 0.f;  // row sum = l + l2
 
-  if (n_tiles > 0) {
-    gload(0);
-    sstore(smem);
-  }
-  __syncthreads();
+  vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
+  const int pro = min(C::NST - 1, n_tiles);
+  for (int t = 0; t < pro; ++t) issue(t);
 
+  const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
   for (int t = 0; t < n_tiles; ++t) {
-    const int n0 = t * BN;
-    if (t + 1 < n_tiles) gload(n0 + BN);
-    const uint16_t* ks = smem + (t & 1) * C::BUF;
-    const uint16_t* vt = ks + C::KBUF;
+    wait_prefill_tile<C::NST, 2 * C::NW>(min(C::NST - 2, n_tiles - 1 - t));
+    __syncthreads();  // tile t is in LDS for every wave; stage (t-1) % NST is free
+    if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
 
-    if (n0 < wave_kend) {
-      f32x16 s[C::MT];
+    const int n0 = t * BN;
+    if (n0 >= wave_kend) continue;  // wave-uniform: every row of the wave is done
+    const uint16_t* ks = ring + (t % C::NST) * C::STAGE;
+    const uint16_t* vs = ks + C::TILE;
+
+    f32x16 s[C::MT];
 #pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
 #pragma unroll
-      for (int kk = 0; kk < C::KK; ++kk) {
+    for (int kk = 0; kk < C::KK; ++kk) {
 #pragma unroll
-        for (int mt2 = 0; mt2 < C::MT; ++mt2) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (32 * mt2 + l32) * C::KSTR + 16 * kk + 8 * hl);
-          s[mt2] = E::mfma(a, qf[kk], s[mt2]);
-        }
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) {
+        const int row = 32 * mt2 + l32;
+        const int sl = (2 * kk + hl) ^ (row & C::SWZ);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
+        s[mt2] = E::mfma(a, qf[kk], s[mt2]);
       }
-      // mask (tiles crossing the diagonal or the key tail only) and row max
-      float mx = -INFINITY;
-      if (n0 + BN - 1 > wave_lim0) {
-#pragma unroll
-        for (int mt2 = 0; mt2 < C::MT; ++mt2)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int key = n0 + 32 * mt2 + 8 * (e >> 2) + 4 * hl + (e & 3);
-            s[mt2][e] = key <= lim ? s[mt2][e] : -INFINITY;
-          }
-      }
+    }
+    // mask (tiles crossing the diagonal or the key tail only) and row max
+    if (n0 + BN - 1 > wave_lim0) {
 #pragma unroll
       for (int mt2 = 0; mt2 < C::MT; ++mt2)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt2][e]);
-      const float mxs = xhalf_max(mx) * c;
-      const bool grow = mxs > m + kLazyRescale;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float m_new = grow ? mxs : m;
-        const float alpha = grow ? exp2_fast(m - m_new) : 1.f;  // 0 when m was -inf
-        l *= alpha;
+        for (int e = 0; e < 16; ++e) {
+          const int key = n0 + 32 * mt2 + 8 * (e >> 2) + 4 * hl + (e & 3);
+          s[mt2][e] = key <= lim ? s[mt2][e] : -INFINITY;
+        }
+    }
+    float mx = max16(s[0]);
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
-        m = m_new;
-      }
-      const float neg_m = m == -INFINITY ? 0.f : -m;
+    for (int mt2 = 1; mt2 < C::MT; ++mt2) mx = max3f(mx, max16(s[mt2]), mx);
+    const float mxs = xhalf_max(mx) * c;
+    const bool grow = mxs > m + kLazyRescale;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mxs : m;
+      const float alpha = grow ? exp2_fast(m - m_new) : 1.f;  // 0 when m was -inf
+      l *= alpha;
+      l2 *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+      m = m_new;
+    }
+    const float neg_m = m == -INFINITY ? 0.f : -m;
 
-      u32x4 pb[2 * C::MT];
+    u32x4 pb[2 * C::MT];
 #pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) {
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) {
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
+      for (int e = 0; e < 16; ++e) s[mt2][e] = exp2_fast(fmaf(s[mt2][e], c, neg_m));
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const int e0 = 8 * cc + 2 * w;
-            const float p0 = exp2_fast(fmaf(s[mt2][e0], c, neg_m));
-            const float p1 = exp2_fast(fmaf(s[mt2][e0 + 1], c, neg_m));
-            l += p0 + p1;
-            pb[2 * mt2 + cc][w] = E::pack2(p0, p1);
-          }
+      for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t pk = E::pack2(s[mt2][8 * cc + 2 * w], s[mt2][8 * cc + 2 * w + 1]);
+          pb[2 * mt2 + cc][w] = pk;
+          if (w & 1) l2 = E::sum2(pk, l2);  // two independent accumulation chains
+          else l = E::sum2(pk, l);
         }
-      }
+    }
 #pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
-        const int drow = 32 * dt + l32;
+    for (int dt = 0; dt < C::DT; ++dt) {
+      int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
+      if (D < 32) d = min(d, D - 4);  // rows >= D of O^T are discarded
+      const int chunk = d >> 3, within = d & 7;
 #pragma unroll
-        for (int cc = 0; cc < 2 * C::MT; ++cc) {
-          u32x4 a = {0u, 0u, 0u, 0u};
-          if (D >= 32 || drow < D) {
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(vt + drow * C::VSTR + 16 * cc + 4 * hl);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(vt + drow * C::VSTR + 16 * cc + 8 + 4 * hl);
-            a = u32x4{lo[0], lo[1], hi[0], hi[1]};
-          }
-          acc[dt] = E::mfma(a, pb[cc], acc[dt]);
-        }
+      for (int cc = 0; cc < 2 * C::MT; ++cc) {
+        const int tlo = 16 * cc + 4 * hl + (rq >> 2);
+        const int thi = tlo + 8;
+        const u32x2 lo = lds_read_tr16(vs + (tlo * C::S + (chunk ^ (tlo & C::SWZ))) * 8 + within);
+        const u32x2 hi = lds_read_tr16(vs + (thi * C::S + (chunk ^ (thi & C::SWZ))) * 8 + within);
+        acc[dt] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[cc], acc[dt]);
       }
     }
-
-    if (t + 1 < n_tiles) sstore(smem + ((t + 1) & 1) * C::BUF);
-    __syncthreads();
   }
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
   // reference's softmax over an all -inf row; Lk == 0 gives zeros.
-  const float l_tot = xhalf_sum(l);
+  const float l_tot = xhalf_sum(l + l2);
   const float inv = p.Lk == 0 ? 0.f : 1.f / l_tot;
   if (qi < p.Lq) {
     uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)qi * p.os2;
