@@ -190,6 +190,27 @@ __device__ __forceinline__ void vm_wait() {
 
 __device__ __forceinline__ void lgkm_wait0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// XOR swizzle of the 16-byte chunks of row r in an LDS tile with S chunks per
+// row. LDS is 64 banks x 4 bytes (256-byte bank rows), so a row of S chunks
+// covers S/16 of a bank row and rows r, r + 16/S, ... share bank columns. Two
+// access patterns must be conflict-free:
+//   ds_read_b128 of one chunk from 16 consecutive rows, and
+//   ds_read_b64_tr_b16 of 4 consecutive chunks from 4 consecutive rows,
+// so rows sharing bank columns get distinct swizzles (bijective within each
+// bank-sharing class) and the swizzles of consecutive such rows differ in the
+// high bits (bit reversal), which moves a 4-chunk run to another bank quarter.
+__device__ __forceinline__ int bitrev3(int x) { return ((x & 1) << 2) | (x & 2) | ((x >> 2) & 1); }
+__device__ __forceinline__ int bitrev4(int x) {
+  return ((x & 1) << 3) | ((x & 2) << 1) | ((x >> 1) & 2) | ((x >> 3) & 1);
+}
+template <int S>
+__device__ __forceinline__ int chunk_swizzle(int r) {
+  if constexpr (S >= 16) return bitrev4(r & 15);
+  else if constexpr (S == 8) return bitrev3((r >> 1) & 7);
+  else if constexpr (S == 4) return (r >> 2) & 3;
+  else return (r >> 3) & 1;
+}
+
 // Transpose helpers for 16-bit data held two per dword: from four rows
 // r0..r3 (dword w covers columns 2w, 2w+1) build the 4 keys of column 2w
 // (even) or 2w+1 (odd) as an 8-byte [r0 r1 r2 r3] pair of dwords.

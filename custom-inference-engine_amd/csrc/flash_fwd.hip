@@ -8,9 +8,9 @@
 //
 // Memory path: each K/V tile (BN keys) is copied global -> LDS by 16-byte
 // direct-to-LDS loads issued by all four waves (no VGPR staging), row-major
-// with the 16-byte chunks of row r XOR-swizzled by (r & 7). NST-1 tiles are in
-// flight while one is computed; one workgroup barrier per tile both publishes
-// the new tile and frees the stage that is refilled next.
+// with the 16-byte chunks of each row XOR-swizzled (chunk_swizzle). NST-2 tiles are in
+// flight while two are resident; one workgroup barrier per tile both publishes
+// the next tile and frees the stage that is refilled next.
 // Per tile and wave:
 //   S^T[BN x 32] = K_tile . Q_w^T     MFMA 32x32x16; A = ds_read_b128 of K rows,
 //                                      B = Q^T resident in registers
@@ -37,23 +37,27 @@ constexpr float kLazyRescale = 8.0f;  // log2 of the largest p tolerated before 
 template <int D>
 struct FlashCfg {
   static constexpr int BM = 128;                                   // query rows per workgroup
-  static constexpr int BN = D <= 32 ? 128 : (D <= 128 ? 64 : 32);  // keys per tile
+  static constexpr int BN = D <= 32 ? 128 : (D == 64 ? 64 : 32);   // keys per tile
   static constexpr int S = D / 8;                                  // 16-byte chunks per row
-  static constexpr int SWZ = (S < 8 ? S : 8) - 1;                  // row swizzle mask
   static constexpr int DT = D >= 32 ? D / 32 : 1;                  // 32-row output tiles
   static constexpr int KK = D / 16;                                // MFMA steps over head_dim
   static constexpr int MT = BN / 32;                               // 32-key score tiles
   static constexpr int TILE = BN * D;                              // elements of one tensor tile
   static constexpr int STAGE = 2 * TILE;                           // K tile, then V tile
-  static constexpr int NST = D <= 64 ? 3 : 2;                      // ring stages
+  static constexpr int NST = D == 256 ? 3 : 4;                     // 2 resident + NST-2 in flight
   static constexpr int NW = BN * S / 256;                          // 1 KiB copies per wave per tensor
-  static constexpr int OCC = D <= 64 ? 3 : (D == 128 ? 2 : 1);     // workgroups per CU
+  static constexpr int PER_TILE = 2 * NW;                          // copies per wave per tile
+  static constexpr int OCC = D <= 128 ? 2 : 1;                     // workgroups per CU
+  static constexpr int NQK = KK * MT;                              // QK^T MFMAs per tile
+  static constexpr int NPV = DT * 2 * MT;                          // P.V MFMAs per tile
   static_assert(NW >= 1 && BN * S == NW * 256, "tile must split evenly over 4 waves");
 };
 
+// vm_wait for the copies of `ahead` tiles issued after the one needed.
 template <int NST, int PER_TILE>
-__device__ __forceinline__ void wait_prefill_tile(int ahead) {
-  if (NST > 2 && ahead >= 1) vm_wait<(NST > 2 ? 1 : 0) * PER_TILE>();
+__device__ __forceinline__ void wait_ahead(int ahead) {
+  if (NST > 3 && ahead >= 2) vm_wait<(NST > 3 ? 2 : 0) * PER_TILE>();
+  else if (NST > 2 && ahead == 1) vm_wait<PER_TILE>();
   else vm_wait<0>();
 }
 
@@ -113,14 +117,14 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   const int last_key = max(p.Lk - 1, 0);
 
   // Tile copy: copy j of this wave moves 16-byte chunk P = (wave*NW + j)*64 + lane
-  // of the tile, i.e. row P / S, chunk (P % S) XOR (row & 7). Rows past the
-  // last key are clamped to it (masked as scores, zero weight in P.V).
+  // of the tile, i.e. row P / S, chunk (P % S) XOR chunk_swizzle(row). Rows
+  // past the last key are clamped to it (masked as scores, zero weight in P.V).
   int lrow[C::NW], lchk[C::NW];
 #pragma unroll
   for (int j = 0; j < C::NW; ++j) {
     const int P = (wave * C::NW + j) * 64 + lane;
     lrow[j] = P / C::S;
-    lchk[j] = 8 * ((P % C::S) ^ (lrow[j] & C::SWZ));
+    lchk[j] = 8 * ((P % C::S) ^ chunk_swizzle<C::S>(lrow[j]));
   }
   auto issue = [&](int t) {
     const int n0 = t * BN;
@@ -133,27 +137,10 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     }
   };
 
-  f32x16 acc[C::DT];
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f, l2 = 0.f;  // row sum = l + l2
-
-  vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
-  const int pro = min(C::NST - 1, n_tiles);
-  for (int t = 0; t < pro; ++t) issue(t);
-
-  const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
-  for (int t = 0; t < n_tiles; ++t) {
-    wait_prefill_tile<C::NST, 2 * C::NW>(min(C::NST - 2, n_tiles - 1 - t));
-    __syncthreads();  // tile t is in LDS for every wave; stage (t-1) % NST is free
-    if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
-
-    const int n0 = t * BN;
-    if (n0 >= wave_kend) continue;  // wave-uniform: every row of the wave is done
+  // S^T of tile t from its ring stage (rows past the tile data are finite
+  // copies of the last key or stale LDS; the caller masks or discards them).
+  auto qk = [&](int t, f32x16* s) {
     const uint16_t* ks = ring + (t % C::NST) * C::STAGE;
-    const uint16_t* vs = ks + C::TILE;
-
-    f32x16 s[C::MT];
 #pragma unroll
     for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
 #pragma unroll
@@ -161,12 +148,16 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 #pragma unroll
       for (int mt2 = 0; mt2 < C::MT; ++mt2) {
         const int row = 32 * mt2 + l32;
-        const int sl = (2 * kk + hl) ^ (row & C::SWZ);
+        const int sl = (2 * kk + hl) ^ chunk_swizzle<C::S>(row);
         const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
         s[mt2] = E::mfma(a, qf[kk], s[mt2]);
       }
     }
-    // mask (tiles crossing the diagonal or the key tail only) and row max
+  };
+  // Bottom-right causal / key-tail mask of tile t (only tiles that cross the
+  // smallest visible limit of the wave need it).
+  auto mask = [&](int t, f32x16* s) {
+    const int n0 = t * BN;
     if (n0 + BN - 1 > wave_lim0) {
 #pragma unroll
       for (int mt2 = 0; mt2 < C::MT; ++mt2)
@@ -176,9 +167,46 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
           s[mt2][e] = key <= lim ? s[mt2][e] : -INFINITY;
         }
     }
+  };
+  auto rowmax = [&](const f32x16* s) {
     float mx = max16(s[0]);
 #pragma unroll
-    for (int mt2 = 1; mt2 < C::MT; ++mt2) mx = max3f(mx, max16(s[mt2]), mx);
+    for (int mt2 = 1; mt2 < C::MT; ++mt2) mx = maxf(mx, max16(s[mt2]));
+    return mx;
+  };
+
+  f32x16 acc[C::DT];
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
+  float m = -INFINITY, l = 0.f, l2 = 0.f;  // row sum = l + l2
+
+  vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
+  const int pro = min(C::NST - 1, n_tiles);
+  for (int t = 0; t < pro; ++t) issue(t);
+
+  // Software pipeline: iteration t holds S(t) in registers, computes
+  // S(t+1) = K(t+1) Q^T while turning S(t) into P(t), then O += V(t) P(t)
+  // while reducing the row max of S(t+1). Tiles t and t+1 are resident; the
+  // copies of the next NST-2 tiles are in flight.
+  f32x16 sc[C::MT];
+  float mx = -INFINITY;
+  if (n_tiles > 0) {
+    wait_ahead<C::NST, C::PER_TILE>(pro - 1);
+    __syncthreads();
+    qk(0, sc);
+    mask(0, sc);
+    mx = rowmax(sc);
+  }
+  const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 1 < n_tiles) {
+      wait_ahead<C::NST, C::PER_TILE>(min(C::NST - 3, n_tiles - 2 - t));
+      __syncthreads();  // tile t+1 resident for all waves; stage of tile t-1 free
+      if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
+    }
+    if (t * BN >= wave_kend) continue;  // wave-uniform: every row of the wave is done
+
+    // lazy rescale against the row max of S(t)
     const float mxs = xhalf_max(mx) * c;
     const bool grow = mxs > m + kLazyRescale;
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -192,35 +220,81 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     }
     const float neg_m = m == -INFINITY ? 0.f : -m;
 
+    // (c) S(t+1) on the MFMA pipe, P(t) on the VALU, interleaved by hand:
+    // after each QK MFMA the next EPC elements of S(t) become probabilities.
+    // sched_barrier(0) keeps the compiler from regrouping the MFMAs. For the
+    // last tile the stage read is stale and S(t+1) is discarded. The empty
+    // volatile asm consumes each packed pair inside its chunk; without it the
+    // softmax would be sunk next to the P.V MFMAs that use it.
+    f32x16 sn[C::MT];
     u32x4 pb[2 * C::MT];
+    {
+      const uint16_t* ks = ring + ((t + 1) % C::NST) * C::STAGE;
+      u32x4 ka[C::NQK];
 #pragma unroll
-    for (int mt2 = 0; mt2 < C::MT; ++mt2) {
+      for (int i = 0; i < C::NQK; ++i) {
+        const int kk = i / C::MT, mt2 = i % C::MT;
+        const int row = 32 * mt2 + l32;
+        const int sl = (2 * kk + hl) ^ chunk_swizzle<C::S>(row);
+        ka[i] = *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
+      }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[mt2][e] = exp2_fast(fmaf(s[mt2][e], c, neg_m));
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = f32x16{};
+      constexpr int EPC = 16 * C::MT / C::NQK;  // S(t) elements per MFMA
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc)
+      for (int i = 0; i < C::NQK; ++i) {
+        const int kk = i / C::MT, mt2 = i % C::MT;
+        sn[mt2] = E::mfma(ka[i], qf[kk], sn[mt2]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t pk = E::pack2(s[mt2][8 * cc + 2 * w], s[mt2][8 * cc + 2 * w + 1]);
-          pb[2 * mt2 + cc][w] = pk;
-          if (w & 1) l2 = E::sum2(pk, l2);  // two independent accumulation chains
-          else l = E::sum2(pk, l);
+        for (int e = i * EPC; e < (i + 1) * EPC; ++e) {
+          const int m2 = e / 16, ee = e % 16;
+          sc[m2][ee] = exp2_fast(fmaf(sc[m2][ee], c, neg_m));
+          if (ee & 1) {  // a pair is complete: pack it and add it to the row sum
+            const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
+            asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
+            pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
+            if (ee & 2) l2 = E::sum2(pk, l2);
+            else l = E::sum2(pk, l);
+          }
         }
-    }
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) {
-      int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
-      if (D < 32) d = min(d, D - 4);  // rows >= D of O^T are discarded
-      const int chunk = d >> 3, within = d & 7;
-#pragma unroll
-      for (int cc = 0; cc < 2 * C::MT; ++cc) {
-        const int tlo = 16 * cc + 4 * hl + (rq >> 2);
-        const int thi = tlo + 8;
-        const u32x2 lo = lds_read_tr16(vs + (tlo * C::S + (chunk ^ (tlo & C::SWZ))) * 8 + within);
-        const u32x2 hi = lds_read_tr16(vs + (thi * C::S + (chunk ^ (thi & C::SWZ))) * 8 + within);
-        acc[dt] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[cc], acc[dt]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+
+    mask(t + 1, sn);
+
+    // (d) O += V(t) P(t) on the MFMA pipe, row max of S(t+1) on the VALU.
+    {
+      const uint16_t* vs = ring + (t % C::NST) * C::STAGE + C::TILE;
+      u32x4 va[C::NPV];
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) {
+        int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
+        if (D < 32) d = min(d, D - 4);  // rows >= D of O^T are discarded
+        const int chunk = d >> 3, within = d & 7;
+#pragma unroll
+        for (int cc = 0; cc < 2 * C::MT; ++cc) {
+          const int tlo = 16 * cc + 4 * hl + (rq >> 2);
+          const int thi = tlo + 8;
+          const u32x2 lo = lds_read_tr16(vs + (tlo * C::S + (chunk ^ chunk_swizzle<C::S>(tlo))) * 8 + within);
+          const u32x2 hi = lds_read_tr16(vs + (thi * C::S + (chunk ^ chunk_swizzle<C::S>(thi))) * 8 + within);
+          va[dt * 2 * C::MT + cc] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < C::NPV; ++i) {
+        const int dt = i % C::DT, cc = i / C::DT;  // alternate accumulators
+        acc[dt] = E::mfma(va[dt * 2 * C::MT + cc], pb[cc], acc[dt]);
+        if (i == C::NPV / 2) {
+          __builtin_amdgcn_sched_barrier(0);
+          mx = rowmax(sn);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) sc[mt2] = sn[mt2];
   }
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the

@@ -15,8 +15,8 @@
 // Memory path: the split's block ids are staged in LDS; K and V tiles of 32
 // tokens are copied global -> LDS by 16-byte direct-to-LDS loads into a ring
 // of NST stages (NST-1 tiles in flight, no VGPR staging). Rows are stored
-// with their 16-byte chunks XOR-swizzled by (token & 7) so the fragment reads
-// below are conflict-free.
+// with their 16-byte chunks XOR-swizzled (chunk_swizzle) so the fragment
+// reads below are conflict-free.
 // Per tile:
 //   S^T[32 x 32] = K_tile . Q^T    A operand: ds_read_b128 of one token row
 //   online softmax in registers (one v_permlane32_swap per reduction)
@@ -35,7 +35,6 @@ struct PagedCfg {
   static constexpr int KK = D / 16;
   static constexpr int DT = D >= 32 ? D / 32 : 1;
   static constexpr int S = D / 8;                         // 16-byte chunks per token row
-  static constexpr int SWZ = (S < 8 ? S : 8) - 1;         // row swizzle mask
   static constexpr int NDMA = S / 2;                      // 1 KiB loads per tensor per tile
   static constexpr int NST = D <= 64 ? 3 : 2;
   static constexpr int TILE = kPagedTile * D;             // elements of one tensor tile
@@ -127,7 +126,7 @@ __global__ __launch_bounds__(64) void paged_fwd_kernel(const PagedParams p) {
   for (int j = 0; j < C::NDMA; ++j) {
     const int P = 64 * j + lane;
     ltok[j] = P / C::S;
-    lchk[j] = 8 * ((P % C::S) ^ (ltok[j] & C::SWZ));
+    lchk[j] = 8 * ((P % C::S) ^ chunk_swizzle<C::S>(ltok[j]));
   }
   // Copy tile k (tokens split0 + 32k ...) into ring stage k % NST. Tokens past
   // the split are clamped to its last token (masked as scores, zero weight).
@@ -179,7 +178,7 @@ __global__ __launch_bounds__(64) void paged_fwd_kernel(const PagedParams p) {
     f32x16 sc = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) {
-      const int slot = (2 * kk + hl) ^ (l32 & C::SWZ);
+      const int slot = (2 * kk + hl) ^ chunk_swizzle<C::S>(l32);
       const u32x4 a = *reinterpret_cast<const u32x4*>(kst + (l32 * C::S + slot) * 8);
       sc = E::mfma(a, qf[kk], sc);
     }
@@ -225,8 +224,8 @@ __global__ __launch_bounds__(64) void paged_fwd_kernel(const PagedParams p) {
       for (int cc = 0; cc < 2; ++cc) {
         const int tlo = 16 * cc + 4 * hl + (rq >> 2);
         const int thi = tlo + 8;
-        const u32x2 lo = lds_read_tr16(vst + (tlo * C::S + (chunk ^ (tlo & C::SWZ))) * 8 + within);
-        const u32x2 hi = lds_read_tr16(vst + (thi * C::S + (chunk ^ (thi & C::SWZ))) * 8 + within);
+        const u32x2 lo = lds_read_tr16(vst + (tlo * C::S + (chunk ^ chunk_swizzle<C::S>(tlo))) * 8 + within);
+        const u32x2 hi = lds_read_tr16(vst + (thi * C::S + (chunk ^ chunk_swizzle<C::S>(thi))) * 8 + within);
         acc[dt] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[cc], acc[dt]);
       }
     }
