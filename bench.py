@@ -48,7 +48,43 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only a 256 MiB copy (counter calibration) and the prefill kernel, "
+                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     return ap.parse_args()
+
+
+TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "flash_fwd_prefill_s2048_traffic.txt")
+
+
+def traffic_from_summary():
+    """HBM bytes per launch of the prefill kernel from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the counter's reading for
+    a copy of known size), or None when no summary is committed."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
+def traffic_probe():
+    import torch
+
+    from benchmarks import workloads
+
+    dev = torch.device("cuda:0")
+    x = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)  # 256 MiB read + 256 MiB written per dispatch
+    fl = FlashLaunch(workloads.prefill_s2048(), dev)
+    for _ in range(3):
+        fl()
+    torch.cuda.synchronize()
+    print("traffic probe done", flush=True)
 
 
 class FlashLaunch:
@@ -158,6 +194,9 @@ def cpu_baseline(case):
 
 def main():
     args = parse()
+    if args.traffic_probe:
+        traffic_probe()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
         sys.exit(2)
@@ -188,7 +227,7 @@ def main():
     kern_ms = event_time_ms(fl, max(20, args.steps), 3)
     achieved = case.flops / (kern_ms / 1e3) / 1e12
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": traffic_from_summary(),
             "kernel": "flash_fwd_kernel<fp16, D=64>", "kernel_us": round(kern_ms * 1e3, 2)}
 
     extra = {}

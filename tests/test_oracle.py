@@ -224,10 +224,10 @@ def _mutant(kind):
             else:
                 hide = j > (Lk - Lq + i)
             s = s.masked_fill(hide, float("-inf"))
-        p = torch.softmax(s, -1)
+        p = torch.softmax(s, -2 if kind == "softmax_over_queries" else -1)
         if kind == "unnormalised":
             p = torch.exp(s - s.amax(-1, keepdim=True))
-        return p @ v
+        return p @ (k if kind == "k_for_v" else v)
     return fn
 
 
@@ -236,7 +236,8 @@ def test_oracle_passes_closed_forms():
     assert closed_form_failures(lambda *a, **kw: torch.from_numpy(attention_brute_f64(*a, **kw)).float()) == []
 
 
-@pytest.mark.parametrize("kind", ["gqa_tile", "top_left", "off_by_one", "no_scale", "unnormalised"])
+@pytest.mark.parametrize("kind", ["gqa_tile", "top_left", "off_by_one", "no_scale", "unnormalised",
+                                  "softmax_over_queries", "k_for_v"])
 def test_planted_mistakes_are_caught(kind):
     assert closed_form_failures(_mutant(kind)), f"mutant {kind} passed every check"
 
