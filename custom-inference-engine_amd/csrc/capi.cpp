@@ -132,16 +132,10 @@ int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
   return launch_status(cie::launch_flash(p, dtype, D, static_cast<hipStream_t>(stream)));
 }
 
-static int paged_geometry(int B, int Hq, int Hk, int Lq, int max_context, int block_size,
-                          int max_blocks_per_seq, int* split_len, int* n_splits) {
+// Largest valid context length: the table bound, tightened by the caller's hint.
+static int paged_ctx_limit(int max_context, int block_size, int max_blocks_per_seq) {
   const int64_t bound = (int64_t)max_blocks_per_seq * block_size;
-  int64_t mc = max_context > 0 ? std::min<int64_t>(max_context, bound) : bound;
-  if (mc < 1) mc = 1;
-  const int R = (Hq / Hk) * Lq;
-  const int n_qt = (R + 31) / 32;
-  *split_len = cie::paged_split_len(B, Hk, n_qt, (int)mc, block_size);
-  *n_splits = (int)((mc + *split_len - 1) / *split_len);
-  return CIE_OK;
+  return (int)(max_context > 0 ? std::min<int64_t>(max_context, bound) : bound);
 }
 
 size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D, int max_context,
@@ -150,10 +144,9 @@ size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D, int max_c
       Hq % Hk)
     return 0;
   if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff) return 0;
-  int split_len = 0, n_splits = 0;
-  paged_geometry(B, Hq, Hk, Lq, max_context, block_size, max_blocks_per_seq, &split_len, &n_splits);
-  if (n_splits <= 1) return 0;
-  return (size_t)B * Hq * Lq * n_splits * (D + 2) * sizeof(float);
+  const cie::PagedGeom g =
+      cie::paged_geometry(B, Hq, Hk, Lq, D, paged_ctx_limit(max_context, block_size, max_blocks_per_seq), block_size);
+  return g.ok ? g.info_bytes + g.slot_bytes : 0;
 }
 
 int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -188,55 +181,54 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   CIE_TRY(check_strides("k_cache", kc_stride));
   CIE_TRY(check_strides("v_cache", vc_stride));
 
-  cie::PagedParams p{};
-  int split_len = 0, n_splits = 0;
-  paged_geometry(B, Hq, Hk, Lq, max_context, block_size, max_blocks_per_seq, &split_len, &n_splits);
-  const size_t need = n_splits > 1 ? (size_t)B * Hq * Lq * n_splits * (D + 2) * sizeof(float) : 0;
-  if (need) {
-    if (!workspace || workspace_bytes < need)
-      return fail(CIE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
-                  workspace ? workspace_bytes : (size_t)0);
-    if (!aligned16(workspace)) return fail(CIE_EINVAL, "workspace: pointer is not 16-byte aligned");
-    p.ws_acc = static_cast<float*>(workspace);
-    p.ws_ml = p.ws_acc + (size_t)B * Hq * Lq * n_splits * D;
-  }
-  const int R = (Hq / Hk) * Lq;
-  const int n_qt = (R + 31) / 32;
-  if ((int64_t)B * n_splits * n_qt * Hk > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
+  const int ctx_limit = paged_ctx_limit(max_context, block_size, max_blocks_per_seq);
+  if ((int64_t)B * ((ctx_limit + 31) / 32) > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
+  const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size);
+  if (!g.ok) return fail(CIE_EINVAL, "paged attention: %s", g.err);
+  const size_t need = g.info_bytes + g.slot_bytes;
+  if (!workspace || workspace_bytes < need)
+    return fail(CIE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!aligned16(workspace)) return fail(CIE_EINVAL, "workspace: pointer is not 16-byte aligned");
 
+  cie::PagedParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.kc = static_cast<const uint16_t*>(k_cache);
   p.vc = static_cast<const uint16_t*>(v_cache);
   p.o = static_cast<uint16_t*>(o);
   p.bt = block_tables;
   p.lens = context_lens;
+  p.info = static_cast<int4*>(workspace);
+  p.slots = reinterpret_cast<float*>(static_cast<char*>(workspace) + g.info_bytes);
   p.qs0 = q_stride[0]; p.qs1 = q_stride[1]; p.qs2 = q_stride[2];
   p.ks0 = kc_stride[0]; p.ks1 = kc_stride[1]; p.ks2 = kc_stride[2];
   p.vs0 = vc_stride[0]; p.vs1 = vc_stride[1]; p.vs2 = vc_stride[2];
   p.os0 = o_stride[0]; p.os1 = o_stride[1]; p.os2 = o_stride[2];
-  p.B = B; p.Hq = Hq; p.Hk = Hk; p.Lq = Lq; p.group = Hq / Hk; p.R = R;
+  p.B = B; p.Hq = Hq; p.Hk = Hk; p.Lq = Lq; p.group = Hq / Hk; p.R = g.R; p.Rt = g.Rt;
   p.num_blocks = num_blocks;
   p.max_blocks = max_blocks_per_seq;
   p.block_size = block_size;
+  p.ctx_limit = ctx_limit;
   p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
   {
-    // Largest element offset of either pool relative to its kv-head base.
-    const int64_t ext_k = (int64_t)(num_blocks > 0 ? num_blocks - 1 : 0) * kc_stride[0] +
-                          (int64_t)(block_size - 1) * kc_stride[1] + (int64_t)D;
-    const int64_t ext_v = (int64_t)(num_blocks > 0 ? num_blocks - 1 : 0) * vc_stride[0] +
-                          (int64_t)(block_size - 1) * vc_stride[1] + (int64_t)D;
+    // Largest element offset of either pool from its base, and the 24-bit
+    // multiplier bounds of the narrow address path.
+    const int64_t nb1 = num_blocks > 0 ? num_blocks - 1 : 0;
+    const int64_t ext_k = nb1 * kc_stride[0] + (int64_t)(block_size - 1) * kc_stride[1] +
+                          (int64_t)(Hk - 1) * kc_stride[2] + (int64_t)D;
+    const int64_t ext_v = nb1 * vc_stride[0] + (int64_t)(block_size - 1) * vc_stride[1] +
+                          (int64_t)(Hk - 1) * vc_stride[2] + (int64_t)D;
     const int64_t lim24 = (int64_t)1 << 24;
     p.narrow = ext_k < ((int64_t)1 << 31) && ext_v < ((int64_t)1 << 31) && num_blocks < lim24 &&
-               kc_stride[0] < lim24 && kc_stride[1] < lim24 && vc_stride[0] < lim24 && vc_stride[1] < lim24;
+               block_size < lim24 && kc_stride[0] < lim24 && kc_stride[1] < lim24 && vc_stride[0] < lim24 &&
+               vc_stride[1] < lim24;
     p.ks0_24 = (uint32_t)kc_stride[0]; p.ks1_24 = (uint32_t)kc_stride[1];
     p.vs0_24 = (uint32_t)vc_stride[0]; p.vs1_24 = (uint32_t)vc_stride[1];
   }
-  p.split_len = split_len;
-  p.n_splits = n_splits;
-  p.n_qt = n_qt;
+  p.Hg = g.Hg; p.NG = g.NG; p.n_qt = g.n_qt; p.NWV = g.NWV; p.NCH = g.NCH; p.NST = g.NST; p.Wg = g.Wg;
   set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
-  return launch_status(cie::launch_paged(p, dtype, D, static_cast<hipStream_t>(stream)));
+  return launch_status(cie::launch_paged(p, dtype, D, g.lds_bytes, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -174,6 +174,22 @@ __device__ __forceinline__ void dma16(const void* gptr, void* lds_wave_base) {
   const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_void*)lds_wave_base);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
 }
+// LDS byte address of a pointer into __shared__ memory, as a wave-uniform
+// value. Take it in uniform control flow: the generic-to-LDS cast checks for
+// null, which only the scalar unit can do.
+__device__ __forceinline__ uint32_t lds_addr_of(void* lds_ptr) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_void*)lds_ptr);
+}
+// Same, with the wave-uniform LDS byte address given directly.
+__device__ __forceinline__ void dma16_at(const void* gptr, uint32_t lds_addr) {
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
+}
+// 4-byte variant: lane l's dword lands at LDS byte address lds_addr + 4 * l.
+__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_addr) {
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ u32x2 lds_read_tr16(const void* lds_ptr) {

@@ -29,6 +29,12 @@ struct FlashParams {
 };
 
 // Paged attention over a (num_blocks, block_size, Hk, D) pool.
+//
+// Work split: the kv heads form NG groups of Hg heads; for every group the
+// 32-token tiles of all sequences, concatenated in batch order, are cut into
+// min(Wg, tiles) equal contiguous ranges, one per workgroup (id = j * NG +
+// group). A sequence covered by more than one range leaves partial states in
+// the workspace that a second kernel merges.
 struct PagedParams {
   const uint16_t* q;
   const uint16_t* kc;
@@ -36,32 +42,47 @@ struct PagedParams {
   uint16_t* o;
   const int32_t* bt;
   const int32_t* lens;
-  float* ws_acc;  // [B*Hq*Lq*n_splits][D] unnormalised partial outputs
-  float* ws_ml;   // [B*Hq*Lq*n_splits][2]  (running max, row sum)
+  int4* info;    // [NG][B] pieces of each sequence: first range, count, slot side of piece 0
+  float* slots;  // [Wg][NG][2][NWV][Rt][D + 2] partial (acc, m, l) of split sequences
   int64_t qs0, qs1, qs2;
   int64_t ks0, ks1, ks2;  // block, offset, head
   int64_t vs0, vs1, vs2;
   int64_t os0, os1, os2;
-  int B, Hq, Hk, Lq, group, R;  // R = group * Lq query rows per kv head
+  int B, Hq, Hk, Lq, group, R, Rt;  // R = group * Lq query rows per kv head, Rt = min(R, 32)
   int num_blocks, max_blocks, block_size;
-  int narrow;  // every pool element offset < 2^31, ids and block/offset strides < 2^24
+  int ctx_limit;  // largest valid context length
+  int narrow;     // pool offsets < 2^31 elements, ids and block/offset strides < 2^24
   uint32_t ks0_24, ks1_24, vs0_24, vs1_24;
   FastDiv bsdiv;
-  int split_len, n_splits, n_qt;
+  int Hg, NG, n_qt, NWV, NCH, NST, Wg;
   float scale_log2;  // |scale| * log2(e), never below 1e-30
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
   int causal;
 };
 
-constexpr int kPagedWaves = 4;
-constexpr int kPagedTile = 32;             // keys per wave iteration
-constexpr int kPagedMaxSplitBlocks = 528;  // block ids of one split staged in LDS
-constexpr int kPagedReduceChunk = 256;      // split weights staged per reduction step
+constexpr int kPagedTile = 32;         // tokens per tile
+constexpr int kPagedIds = 384;         // block ids of one workgroup's range staged in LDS
+constexpr int kPagedEntries = 32;      // sequences one workgroup's range may touch
+constexpr int kPagedMaxWaves = 8;      // waves per workgroup
+constexpr int kPagedCUs = 256;         // compute units the launch is sized for
+constexpr int kPagedLdsBudget = 150 * 1024;
 
-// Split length (multiple of kPagedWaves * kPagedTile) for a paged launch.
-int paged_split_len(int B, int Hk, int n_qt, int max_ctx, int block_size);
+// Launch geometry of a paged call; a pure function of the arguments, so the
+// workspace query and the launch agree.
+struct PagedGeom {
+  int ok;            // 0: shape not supported (error text in err)
+  const char* err;
+  int R, Rt, n_qt;
+  int Hg, NG, NWV;   // kv heads per workgroup, head groups, waves per workgroup
+  int NCH;           // 16-byte chunks per token row of a head group (Hg * D / 8)
+  int NST;           // LDS stages
+  int Wg;            // workgroups per head group
+  size_t lds_bytes;  // dynamic LDS per workgroup
+  size_t info_bytes, slot_bytes;  // workspace parts
+};
+PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size);
 
 hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stream);
-hipError_t launch_paged(const PagedParams& p, int dtype, int D, hipStream_t stream);
+hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, hipStream_t stream);
 
 }  // namespace cie

@@ -6,24 +6,39 @@
 // K and V are read once, straight out of the (num_blocks, block_size, Hk, D)
 // pool through the int32 block table.
 //
-// One wave per (sequence, context split, query tile, kv head). The kv heads
-// of one (sequence, split) are adjacent workgroup ids, so the pool blocks they
-// share (block_size * Hk * D contiguous elements) are read at the same time.
-// All Hq/Hk query heads x Lq new tokens of a kv head (R = group * Lq rows, up
-// to 32 per query tile) share each K/V byte.
+// Memory path. A workgroup owns a group of Hg kv heads (Hg * D <= 512, so a
+// token's rows of the group are at most 1 KiB, contiguous in the pool) and
+// one wave per (kv head, query tile). Each 32-token tile of K and of V is
+// copied global -> LDS by 16-byte direct-to-LDS loads, every load instruction
+// covering one contiguous KiB of the pool: whole pool blocks stream at close
+// to copy bandwidth, where per-head 128-byte rows scattered 1 KiB apart do
+// not. The tile is stored token-major with the 16-byte chunks of each token
+// row XOR-swizzled (row_swizzle), so the per-head fragment reads below are
+// bank-conflict-free. NST stages rotate; the copies of the next NST-1 tiles
+// are in flight while one tile is computed.
 //
-// Memory path: the split's block ids are staged in LDS; K and V tiles of 32
-// tokens are copied global -> LDS by 16-byte direct-to-LDS loads into a ring
-// of NST stages (NST-1 tiles in flight, no VGPR staging). Rows are stored
-// with their 16-byte chunks XOR-swizzled (chunk_swizzle) so the fragment
-// reads below are conflict-free.
-// Per tile:
-//   S^T[32 x 32] = K_tile . Q^T    A operand: ds_read_b128 of one token row
+// Per tile and wave (one kv head, up to 32 query rows r = g * Lq + i: query
+// head kvh * group + g, new token i):
+//   S^T[32 keys x 32 rows] = K_tile . Q^T    A operand: ds_read_b128 of a token row
 //   online softmax in registers (one v_permlane32_swap per reduction)
-//   O^T += V^T_tile . P^T          A operand: ds_read_b64_tr_b16 turns the
-//                                   row-major V tile into key-contiguous V^T
-// A wave whose sequence has a single split writes the final output; otherwise
-// it writes (m, l, acc) partials that paged_reduce_kernel combines.
+//   O^T += V^T_tile . P^T                    A operand: ds_read_b64_tr_b16 turns the
+//                                             token-major V tile into key-contiguous V^T
+//
+// Work split (stream-K over sequences). For a head group, the 32-token tiles
+// of all sequences are concatenated in batch order and cut into equal
+// contiguous ranges, one per workgroup, so every workgroup streams the same
+// number of bytes whatever the context lengths. A sequence inside one range
+// is written directly. A sequence cut across ranges leaves one partial state
+// (acc, m, l) per piece in the workspace plus a piece descriptor, and
+// paged_merge_kernel combines the pieces in piece order (the kernel boundary
+// makes the partials visible; no counters or device-wide fences).
+//
+// Invalid input is never dereferenced: a context length outside
+// [0, ctx_limit] or a block id outside [0, num_blocks) makes that sequence's
+// output NaN.
+#include <climits>
+#include <mutex>
+
 #include "kernels.hpp"
 
 namespace cie {
@@ -32,157 +47,365 @@ constexpr float kLazyRescalePaged = 8.0f;
 
 template <int D>
 struct PagedCfg {
-  static constexpr int KK = D / 16;
-  static constexpr int DT = D >= 32 ? D / 32 : 1;
-  static constexpr int S = D / 8;                         // 16-byte chunks per token row
-  static constexpr int NDMA = S / 2;                      // 1 KiB loads per tensor per tile
-  static constexpr int NST = D <= 64 ? 3 : 2;
-  static constexpr int TILE = kPagedTile * D;             // elements of one tensor tile
-  static constexpr int STAGE = 2 * TILE;                  // K tile, then V tile
+  static constexpr int KK = D / 16;                 // MFMA steps over head_dim
+  static constexpr int DT = D >= 32 ? D / 32 : 1;   // 32-row output tiles
+  static constexpr int S = D / 8;                   // 16-byte chunks per head row
+  static constexpr int DPW = D / 16;                // 1 KiB copies per issuing wave, tensor and tile
+  static constexpr int QPRE = D <= 64 ? 3 : (D == 128 ? 1 : 0);  // sequences with q loaded up front
+  static constexpr int QARR = QPRE > 0 ? QPRE : 1;
+  static constexpr int MU = D <= 64 ? 4 : (D == 128 ? 2 : 1);    // pieces loaded together by a merge
 };
 
-template <int N, int NDMA>
+// Swizzle of the 16-byte chunks of token row t in a tile with nch chunks per
+// row: the family of chunk_swizzle applied to rows of nch chunks.
+__device__ __forceinline__ int row_swizzle(int nch, int t) {
+  return nch >= 16 ? bitrev4(t & 15) : nch == 8 ? bitrev3((t >> 1) & 7) : nch == 4 ? ((t >> 2) & 3) : ((t >> 3) & 1);
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+__device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
+  return ctx >= 0 && ctx <= p.ctx_limit && (ctx == 0 || p.num_blocks > 0);
+}
+
+// Range index of tile x when nt tiles are cut into wg <= nt ranges
+// [floor(j nt / wg), floor((j+1) nt / wg)).
+__device__ __forceinline__ int range_of(int x, int nt, int wg) {
+  return (int)(((int64_t)(x + 1) * wg - 1) / nt);
+}
+
+template <int DPW>
 __device__ __forceinline__ void wait_tiles_ahead(int ahead) {
-  // vmcnt counts the 2 * NDMA loads of every tile issued after the one needed
-  if (N > 3 && ahead >= 3) vm_wait<(N > 3 ? 3 : 0) * 2 * NDMA>();
-  else if (N > 2 && ahead == 2) vm_wait<(N > 2 ? 2 : 0) * 2 * NDMA>();
-  else if (N > 1 && ahead == 1) vm_wait<2 * NDMA>();
-  else vm_wait<0>();
+  // vmcnt counts the 2 * DPW copies of every tile issued after the one needed
+  if constexpr (6 * DPW < 64) {
+    if (ahead >= 3) { vm_wait<6 * DPW>(); return; }
+  }
+  if constexpr (4 * DPW < 64) {
+    if (ahead == 2) { vm_wait<4 * DPW>(); return; }
+  }
+  if (ahead == 1) { vm_wait<2 * DPW>(); return; }
+  vm_wait<0>();
+}
+
+// Writes this lane's half (columns [hl * D/2, (hl+1) * D/2)) of one output
+// row with a constant 16-bit pattern.
+template <int D>
+__device__ __forceinline__ void fill_row_half(uint16_t* row, int hl, uint32_t bits2) {
+#pragma unroll
+  for (int d = hl * (D / 2); d < (hl + 1) * (D / 2); d += 8)
+    *reinterpret_cast<u32x4*>(row + d) = u32x4{bits2, bits2, bits2, bits2};
+}
+
+// Stores acc * inv (MFMA C layout of O^T: this lane holds row l32, columns
+// 32 dt + 8 g4 + 4 hl + 0..3) as one output row.
+template <int DTYPE, int D>
+__device__ __forceinline__ void store_row(uint16_t* row, const f32x16* acc, float inv, int hl) {
+  using E = Elt<DTYPE>;
+  constexpr int DT = PagedCfg<D>::DT;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * dt + 8 * g4 + 4 * hl;
+      if (D >= 32 || d < D) {
+        const u32x2 w = {E::pack2(acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv),
+                         E::pack2(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(row + d) = w;
+      }
+    }
+  }
 }
 
 template <int DTYPE, int D>
-__global__ __launch_bounds__(64) void paged_fwd_kernel(const PagedParams p) {
+__global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const PagedParams p) {
   using C = PagedCfg<D>;
   using E = Elt<DTYPE>;
-  __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
-  __shared__ int32_t sbt[kPagedMaxSplitBlocks];
+  extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
+  __shared__ int32_t sbt[kPagedIds];
+  __shared__ int32_t ent[kPagedEntries][8];  // b, ctx, tt_lo, n, idbase, blk_lo, pre, pieces
 
-  // blockIdx.x = ((b * n_splits + s) * n_qt + qt) * Hk + kvh
-  int id = blockIdx.x;
-  const int kvh = id % p.Hk;
-  id /= p.Hk;
-  const int qt = id % p.n_qt;
-  id /= p.n_qt;
-  const int s = id % p.n_splits;
-  const int b = id / p.n_splits;
-  const int lane = threadIdx.x, l32 = lane & 31, hl = lane >> 5;
+  const int gh = blockIdx.x % p.NG;
+  const int j = blockIdx.x / p.NG;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, uniform
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
+  const int hh = w % p.Hg, qt = w / p.Hg;
+  const int kvh = gh * p.Hg + hh;
+  const bool issuer = qt == 0;  // the qt = 0 waves copy the tiles all waves read
 
-  int ctx = p.lens[b];
-  const bool bad_len = ctx < 0 || ctx > p.max_blocks * p.block_size || ctx > p.n_splits * p.split_len ||
-                       (ctx > 0 && p.num_blocks < 1);
-  if (bad_len) ctx = 0;  // never dereference; the output is poisoned below
-  const int nsb = max(1, (ctx + p.split_len - 1) / p.split_len);
-  if (s >= nsb) return;
-  const int split0 = s * p.split_len;
-  const int split1 = min(ctx, split0 + p.split_len);
-  const int ntiles = split1 > split0 ? (split1 - split0 + kPagedTile - 1) / kPagedTile : 0;
-
-  // Query row of this lane: r = g * Lq + i (query head kvh*group + g, token i).
+  // Query row of this lane.
   const int r = qt * 32 + l32;
   const bool rv = r < p.R;
   const int g = rv ? r / p.Lq : 0;
   const int i = rv ? r - g * p.Lq : 0;
   const int hq = kvh * p.group + g;
-  const uint16_t* qrow = p.q + b * p.qs0 + hq * p.qs1 + (int64_t)i * p.qs2;
-  u32x4 qf[C::KK];
-#pragma unroll
-  for (int kk = 0; kk < C::KK; ++kk) {
-    qf[kk] = load16(qrow + 16 * kk + 8 * hl, rv);
-    qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
+  const uint32_t nan2 = 0x7fff7fffu;  // NaN in both fp16 and bf16
+
+  // ---- schedule: every wave derives it from the context lengths ----------
+  int NT = 0;
+  for (int b0 = 0; b0 < p.B; b0 += 64) {
+    const int b = b0 + lane;
+    const int ctx = b < p.B ? p.lens[b] : 0;
+    NT += ctx_valid(p, ctx) ? (ctx + kPagedTile - 1) / kPagedTile : 0;
   }
+  NT = wave_sum_i(NT);
+  // W <= NT ranges, so none is empty: every range a sequence spans holds one
+  // of its pieces (workgroups j >= W have nothing to do).
+  const int W = min(p.Wg, NT);
+  const int S0 = j < W ? (int)((int64_t)j * NT / W) : NT;
+  const int S1 = j < W ? (int)((int64_t)(j + 1) * NT / W) : NT;
 
-  // Stage the split's block ids (validated) in LDS.
-  const int blk0 = ntiles ? (int)fdiv((uint32_t)split0, p.bsdiv) : 0;
-  const int nblk = ntiles ? (int)fdiv((uint32_t)(split1 - 1), p.bsdiv) - blk0 + 1 : 0;
-  bool bad_blk = false;
-  const int32_t* btr = p.bt + (int64_t)b * p.max_blocks;
-  for (int j = lane; j < nblk; j += 64) {
-    const int bid = btr[blk0 + j];
-    const bool inb = bid >= 0 && bid < p.num_blocks;
-    bad_blk |= !inb;
-    sbt[j] = inb ? bid : 0;
-  }
-  const bool any_bad = __builtin_amdgcn_ballot_w64(bad_blk) != 0;
-  // Q and the block ids are in registers / LDS before the first LDS DMA is
-  // issued; an explicit wait here keeps the compiler from draining the DMA
-  // queue inside the tile loop on their account.
-  vm_wait<0>();
-
-  // Last key visible to this row: the Lq new tokens are the newest Lq
-  // positions of the context (bottom-right causal alignment). lim_min is the
-  // smallest lim of the wave; tiles entirely at or below it need no mask.
-  const int lim = min(split1 - 1, p.causal ? ctx - p.Lq + i : ctx - 1);
-  const int lim_min = min(split1 - 1, p.causal ? ctx - p.Lq : ctx - 1);
-  const float c = p.scale_log2;
-
-  const uint16_t* kbase = p.kc + kvh * p.ks2;
-  const uint16_t* vbase = p.vc + kvh * p.vs2;
-  const int last = split1 - 1;
-
-  // Tile copy: load j of a tile moves 16-byte chunk P = 64 j + lane, i.e.
-  // chunk (P % S) XOR swizzle of token P / S. Per-lane parts are fixed.
-  int ltok[C::NDMA], lchk[C::NDMA];
-#pragma unroll
-  for (int j = 0; j < C::NDMA; ++j) {
-    const int P = 64 * j + lane;
-    ltok[j] = P / C::S;
-    lchk[j] = 8 * ((P % C::S) ^ chunk_swizzle<C::S>(ltok[j]));
-  }
-  // Copy tile k (tokens split0 + 32k ...) into ring stage k % NST. Tokens past
-  // the split are clamped to its last token (masked as scores, zero weight).
-  auto issue = [&](int k) {
-    const int t0 = split0 + kPagedTile * k;
-    uint16_t* st = ring + (k % C::NST) * C::STAGE;
-    int bid[C::NDMA], off[C::NDMA];
-#pragma unroll
-    for (int j = 0; j < C::NDMA; ++j) {  // all block-id reads in flight together
-      const int t = min(t0 + ltok[j], last);
-      const uint32_t blk = fdiv((uint32_t)t, p.bsdiv);
-      off[j] = t - (int)blk * p.block_size;
-      bid[j] = sbt[blk - blk0];
+  int ne = 0, nid = 0, carry = 0;
+  for (int b0 = 0; b0 < p.B; b0 += 64) {
+    if (j != 0 && carry >= S1) break;
+    const int b = b0 + lane;
+    const int ctx = b < p.B ? p.lens[b] : 0;
+    const bool valid = ctx_valid(p, ctx);
+    const int t = valid ? (ctx + kPagedTile - 1) / kPagedTile : 0;
+    const int incl = wave_incl_scan(t, lane);
+    const int pre = carry + incl - t;
+    carry += __shfl(incl, 63);
+    if (j == 0) {
+      // Sequences without tiles: zeros for an empty history, NaN for an
+      // invalid length. The first workgroup of each head group writes them.
+      uint64_t zm = __builtin_amdgcn_ballot_w64(b < p.B && t == 0);
+      while (zm) {
+        const int zl = __builtin_ctzll(zm);
+        zm &= zm - 1;
+        const int zvalid = __shfl((int)valid, zl);
+        if (rv) fill_row_half<D>(p.o + (int64_t)(b0 + zl) * p.os0 + hq * p.os1 + (int64_t)i * p.os2, hl,
+                                 zvalid ? 0u : nan2);
+      }
     }
-    if (p.narrow) {  // pool offsets < 2^31 elements, ids and strides < 2^24: 24-bit multiplies
+    if (j == 0 && w == 0 && b < p.B && t == 0)
+      p.info[(int64_t)gh * p.B + b] = int4{0, 0, 0, 0};  // nothing to merge
+    const bool ov = t > 0 && pre < S1 && pre + t > S0;
+    int tt_lo = 0, n = 0, blk_lo = 0, nids = 0;
+    if (ov) {
+      tt_lo = max(S0 - pre, 0);
+      const int tt_hi = min(S1 - pre, t);
+      n = tt_hi - tt_lo;
+      blk_lo = (int)fdiv((uint32_t)(kPagedTile * tt_lo), p.bsdiv);
+      const int blk_hi = (int)fdiv((uint32_t)(min(ctx, kPagedTile * tt_hi) - 1), p.bsdiv);
+      nids = blk_hi - blk_lo + 1;
+    }
+    const int ids_incl = wave_incl_scan(nids, lane);
+    const uint64_t om = __builtin_amdgcn_ballot_w64(ov);
+    if (w == 0 && ov) {
+      const int e = ne + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(om >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)om, 0));
+      const int j0 = range_of(pre, NT, W), j1 = range_of(pre + t - 1, NT, W);
+      ent[e][0] = b;
+      ent[e][1] = ctx;
+      ent[e][2] = tt_lo;
+      ent[e][3] = n;
+      ent[e][4] = nid + ids_incl - nids;
+      ent[e][5] = blk_lo;
+      ent[e][6] = pre;
+      ent[e][7] = j1 - j0 + 1;
+      // The range holding a sequence's first tile describes its pieces for
+      // the merge pass: first range, piece count, slot side of piece 0.
+      if (pre >= S0) p.info[(int64_t)gh * p.B + b] = int4{j, j1 - j0 + 1, pre > S0 ? 1 : 0, 0};
+    }
+    ne += __builtin_popcountll(om);
+    nid += __shfl(ids_incl, 63);
+  }
+  const int T = S1 - S0;
+
+  // Stage the block ids of the range in LDS (one direct-to-LDS dword per id);
+  // ids outside [0, num_blocks) become -1 (never dereferenced, poison the piece).
+  const uint32_t sbt_lds = lds_addr_of(sbt);
+  if (w == 0 && T > 0) {
+    for (int e = 0; e < ne; ++e) {
+      // entry fields are wave-uniform; readfirstlane keeps the address math scalar
+      const int b = __builtin_amdgcn_readfirstlane(ent[e][0]), ctx = __builtin_amdgcn_readfirstlane(ent[e][1]);
+      const int tt_lo = __builtin_amdgcn_readfirstlane(ent[e][2]), n = __builtin_amdgcn_readfirstlane(ent[e][3]);
+      const int idb = __builtin_amdgcn_readfirstlane(ent[e][4]), blk_lo = __builtin_amdgcn_readfirstlane(ent[e][5]);
+      const int blk_hi = (int)fdiv((uint32_t)(min(ctx, kPagedTile * (tt_lo + n)) - 1), p.bsdiv);
+      const int cnt = blk_hi - blk_lo + 1;
+      const int32_t* src = p.bt + (int64_t)b * p.max_blocks + blk_lo;
+      for (int x0 = 0; x0 < cnt; x0 += 64) {
+        const uint32_t dst = sbt_lds + 4u * (uint32_t)(idb + x0);
+        if (x0 + lane < cnt) dma4(src + x0 + lane, dst);
+      }
+    }
+    vm_wait<0>();
+    for (int x = lane; x < nid; x += 64)
+      if ((uint32_t)sbt[x] >= (uint32_t)p.num_blocks) sbt[x] = -1;
+  }
+  __syncthreads();
+  if (T == 0) return;
+
+  // ---- per-lane constants -------------------------------------------------
+  const int NCH = p.NCH, NST = p.NST;
+  const int lg_nch = __builtin_ctz(NCH);
+  const int TILE_EL = kPagedTile * NCH * 8;  // elements of one tensor tile
+  const int STAGE_EL = 2 * TILE_EL;
+
+  // Copies: load i of this wave moves LDS chunk P = 64 (hh DPW + i) + lane of
+  // the tile, i.e. token P / NCH, stored chunk P % NCH, which holds chunk
+  // (P % NCH) ^ row_swizzle(token) of the token's group row.
+  int ltok[C::DPW];
+  int64_t goffk[C::DPW], goffv[C::DPW];
 #pragma unroll
-      for (int j = 0; j < C::NDMA; ++j) {
-        const uint32_t ko = __umul24(bid[j], p.ks0_24) + __umul24(off[j], p.ks1_24) + lchk[j];
-        const uint32_t vo = __umul24(bid[j], p.vs0_24) + __umul24(off[j], p.vs1_24) + lchk[j];
-        dma16(kbase + ko, st + 512 * j);
-        dma16(vbase + vo, st + C::TILE + 512 * j);
+  for (int x = 0; x < C::DPW; ++x) {
+    const int P = 64 * (hh * C::DPW + x) + lane;
+    const int tk = P >> lg_nch;
+    const int c = (P & (NCH - 1)) ^ row_swizzle(NCH, tk);
+    const int hd = c / C::S, dc = c % C::S;
+    ltok[x] = tk;
+    goffk[x] = (int64_t)(gh * p.Hg + hd) * p.ks2 + 8 * dc;
+    goffv[x] = (int64_t)(gh * p.Hg + hd) * p.vs2 + 8 * dc;
+  }
+  // Fragment reads: K row l32 (chunk 2 kk + hl of head hh), V^T rows.
+  const int swk = row_swizzle(NCH, l32);
+  const int rq = lane & 15, gq = lane >> 4;
+  int swv[2][2];
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    swv[cc][0] = row_swizzle(NCH, 16 * cc + 4 * hl + (rq >> 2));
+    swv[cc][1] = row_swizzle(NCH, 16 * cc + 4 * hl + (rq >> 2) + 8);
+  }
+
+  const uint32_t ring_lds = lds_addr_of(ring);  // byte address of stage 0
+
+  // Issue cursor.
+  int ie = 0, i_base = 0, i_end = ent[0][3];
+  int i_ctx = ent[0][1], i_ttlo = ent[0][2], i_idb = ent[0][4], i_blk = ent[0][5];
+  int i_stage = 0;
+  auto issue = [&](int k) {
+    if (k == i_end) {
+      ++ie;
+      i_base = i_end;
+      i_end += ent[ie][3];
+      i_ctx = ent[ie][1];
+      i_ttlo = ent[ie][2];
+      i_idb = ent[ie][4];
+      i_blk = ent[ie][5];
+    }
+    const int tbase = kPagedTile * (i_ttlo + k - i_base);
+    const uint32_t st = ring_lds + 2u * (uint32_t)(i_stage * STAGE_EL) + 1024u * (uint32_t)(hh * C::DPW);
+    i_stage = i_stage + 1 == NST ? 0 : i_stage + 1;
+    int bid[C::DPW], off[C::DPW];
+#pragma unroll
+    for (int x = 0; x < C::DPW; ++x) {  // all block-id reads in flight together
+      const int tk = min(tbase + ltok[x], i_ctx - 1);
+      const int blk = (int)fdiv((uint32_t)tk, p.bsdiv);
+      off[x] = tk - blk * p.block_size;
+      bid[x] = max(sbt[i_idb + blk - i_blk], 0);
+    }
+    if (p.narrow) {
+#pragma unroll
+      for (int x = 0; x < C::DPW; ++x) {
+        const uint32_t base_k = __umul24(bid[x], p.ks0_24) + __umul24(off[x], p.ks1_24);
+        const uint32_t base_v = __umul24(bid[x], p.vs0_24) + __umul24(off[x], p.vs1_24);
+        dma16_at(p.kc + base_k + goffk[x], st + 1024u * x);
+        dma16_at(p.vc + base_v + goffv[x], st + 2u * TILE_EL + 1024u * x);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < C::NDMA; ++j) {
-        dma16(kbase + (int64_t)bid[j] * p.ks0 + (int64_t)off[j] * p.ks1 + lchk[j], st + 512 * j);
-        dma16(vbase + (int64_t)bid[j] * p.vs0 + (int64_t)off[j] * p.vs1 + lchk[j], st + C::TILE + 512 * j);
+      for (int x = 0; x < C::DPW; ++x) {
+        dma16_at(p.kc + (int64_t)bid[x] * p.ks0 + (int64_t)off[x] * p.ks1 + goffk[x], st + 1024u * x);
+        dma16_at(p.vc + (int64_t)bid[x] * p.vs0 + (int64_t)off[x] * p.vs1 + goffv[x], st + 2u * TILE_EL + 1024u * x);
       }
     }
   };
 
-  f32x16 acc[C::DT];
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f;
+  const int pro = min(NST - 1, T);
+  if (issuer)
+    for (int k = 0; k < pro; ++k) issue(k);
 
-  const int pro = min(C::NST - 1, ntiles);
-  for (int k = 0; k < pro; ++k) issue(k);
-  for (int n = 0; n < ntiles; ++n) {
-    if (n + C::NST - 1 < ntiles) {
-      lgkm_wait0();  // the previous tile's LDS reads of the recycled stage are done
-      issue(n + C::NST - 1);
+  // q rows of the first QPRE sequences, loaded while the first tiles arrive.
+  const uint16_t* qrow = p.q + hq * p.qs1 + (int64_t)i * p.qs2;
+  u32x4 qpre[C::QARR][C::KK];
+#pragma unroll
+  for (int e = 0; e < C::QPRE; ++e) {
+    const int b = e < ne ? ent[e][0] : 0;
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) qpre[e][kk] = load16(qrow + b * p.qs0 + 16 * kk + 8 * hl, rv && e < ne);
+  }
+  vm_wait<0>();
+#pragma unroll
+  for (int e = 0; e < C::QPRE; ++e)
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) qpre[e][kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
+
+  // Compute cursor and the running state of the current sequence piece.
+  int ce = -1, c_base = 0, c_end = 0, c_stage = 0;
+  int c_b = 0, c_ctx = 0, c_ttlo = 0, lim = 0, lim_min = 0;
+  bool poison = false;
+  u32x4 qf[C::KK];
+  f32x16 acc[C::DT];
+  float m = -INFINITY, l = 0.f;
+  const float c = p.scale_log2;
+
+  for (int n = 0; n < T; ++n) {
+    if (issuer) {
+      if (n + NST - 1 < T) issue(n + NST - 1);
+      wait_tiles_ahead<C::DPW>(min(NST - 1, T - 1 - n));
     }
-    wait_tiles_ahead<C::NST, C::NDMA>(min(C::NST - 1, ntiles - 1 - n));
-    const uint16_t* kst = ring + (n % C::NST) * C::STAGE;
-    const uint16_t* vst = kst + C::TILE;
-    const int t0 = split0 + kPagedTile * n;
+    __syncthreads();  // tile n is in LDS for every wave
+
+    if (n == c_end) {  // first tile of the next sequence piece
+      ++ce;
+      c_base = n;
+      c_end = n + ent[ce][3];
+      c_b = ent[ce][0];
+      c_ctx = ent[ce][1];
+      c_ttlo = ent[ce][2];
+      {
+        const int idb = ent[ce][4], blk_lo = ent[ce][5];
+        const int blk_hi = (int)fdiv((uint32_t)(min(c_ctx, kPagedTile * (c_ttlo + ent[ce][3])) - 1), p.bsdiv);
+        bool bad = false;
+        for (int x = lane; x < blk_hi - blk_lo + 1; x += 64) bad |= sbt[idb + x] < 0;
+        poison = __builtin_amdgcn_ballot_w64(bad) != 0;
+      }
+      if (ce < C::QPRE) {
+#pragma unroll
+        for (int e = 0; e < C::QPRE; ++e)
+          if (e == ce)
+#pragma unroll
+            for (int kk = 0; kk < C::KK; ++kk) qf[kk] = qpre[e][kk];
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < C::KK; ++kk) {
+          qf[kk] = load16(qrow + c_b * p.qs0 + 16 * kk + 8 * hl, rv);
+          qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
+      m = -INFINITY;
+      l = 0.f;
+      // Last key visible to this row: the Lq new tokens are the newest Lq
+      // positions of the context (bottom-right causal alignment).
+      lim = p.causal ? c_ctx - p.Lq + i : c_ctx - 1;
+      lim_min = p.causal ? c_ctx - p.Lq : c_ctx - 1;
+    }
+
+    const uint16_t* kst = ring + c_stage * STAGE_EL;
+    const uint16_t* vst = kst + TILE_EL;
+    c_stage = c_stage + 1 == NST ? 0 : c_stage + 1;
+    const int t0 = kPagedTile * (c_ttlo + n - c_base);
 
     f32x16 sc = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) {
-      const int slot = (2 * kk + hl) ^ chunk_swizzle<C::S>(l32);
-      const u32x4 a = *reinterpret_cast<const u32x4*>(kst + (l32 * C::S + slot) * 8);
+      const int pos = (hh * C::S + 2 * kk + hl) ^ swk;
+      const u32x4 a = *reinterpret_cast<const u32x4*>(kst + ((l32 << lg_nch) + pos) * 8);
       sc = E::mfma(a, qf[kk], sc);
     }
-
     if (t0 + kPagedTile - 1 > lim_min) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -209,167 +432,221 @@ __global__ __launch_bounds__(64) void paged_fwd_kernel(const PagedParams p) {
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) pb[cc][w] = E::pack2(sc[8 * cc + 2 * w], sc[8 * cc + 2 * w + 1]);
+      for (int x = 0; x < 4; ++x) pb[cc][x] = E::pack2(sc[8 * cc + 2 * x], sc[8 * cc + 2 * x + 1]);
 
-    // V^T fragments: lane (group gq = lane/16, r = lane%16) points at token
-    // k0 + r/4, dims d0 + 4*(r%4); the transpose read hands lane l the four
-    // keys k0..k0+3 of dim 32*dt + lane%32.
-    const int rq = lane & 15, gq = lane >> 4;
+    // V^T fragments: lane (group gq, r = rq) points at token k0 + r/4, dims
+    // d0 + 4 (r % 4); the transpose read hands lane l the four keys k0..k0+3
+    // of dim 32 dt + lane % 32.
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
       int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
       if (D < 32) d = min(d, D - 4);  // rows >= D of O^T are discarded
-      const int chunk = d >> 3, within = d & 7;
+      const int chunk = hh * C::S + (d >> 3), within = d & 7;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
         const int tlo = 16 * cc + 4 * hl + (rq >> 2);
         const int thi = tlo + 8;
-        const u32x2 lo = lds_read_tr16(vst + (tlo * C::S + (chunk ^ chunk_swizzle<C::S>(tlo))) * 8 + within);
-        const u32x2 hi = lds_read_tr16(vst + (thi * C::S + (chunk ^ chunk_swizzle<C::S>(thi))) * 8 + within);
+        const u32x2 lo = lds_read_tr16(vst + ((tlo << lg_nch) + (chunk ^ swv[cc][0])) * 8 + within);
+        const u32x2 hi = lds_read_tr16(vst + ((thi << lg_nch) + (chunk ^ swv[cc][1])) * 8 + within);
         acc[dt] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[cc], acc[dt]);
       }
     }
-  }
 
-  const float l_tot = xhalf_sum(l);
-  if (!rv) return;
-  const bool poisoned = bad_len || any_bad;
-  if (nsb == 1 || poisoned) {
-    const float inv = poisoned ? __builtin_nanf("") : (ctx == 0 ? 0.f : 1.f / l_tot);
-    uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)i * p.os2;
+    if (n == c_end - 1) {  // last tile of the piece
+      const float l_tot = xhalf_sum(l);
+      if (ent[ce][7] == 1) {
+        const float inv = poison ? __builtin_nanf("") : 1.f / l_tot;
+        if (rv) store_row<DTYPE, D>(p.o + (int64_t)c_b * p.os0 + hq * p.os1 + (int64_t)i * p.os2, acc, inv, hl);
+      } else {
+        // Piece of a split sequence: side 1 if it starts inside this range.
+        const int side = ent[ce][6] > S0 ? 1 : 0;
+        float* sl = p.slots + ((((int64_t)j * p.NG + gh) * 2 + side) * p.NWV + w) * p.Rt * (D + 2);
+        const float pz = poison ? __builtin_nanf("") : 1.f;
+        if (rv) {
 #pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) {
+          for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = 32 * dt + 8 * g4 + 4 * hl;
-        if (D >= 32 || d < D) {
-          const u32x2 w = {E::pack2(acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv),
-                           E::pack2(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv)};
-          *reinterpret_cast<u32x2*>(orow + d) = w;
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int d = 32 * dt + 8 * g4 + 4 * hl;
+              if (D >= 32 || d < D)
+                *reinterpret_cast<float4*>(sl + l32 * D + d) =
+                    float4{acc[dt][4 * g4] * pz, acc[dt][4 * g4 + 1] * pz, acc[dt][4 * g4 + 2] * pz,
+                           acc[dt][4 * g4 + 3] * pz};
+            }
+          if (hl == 0) *reinterpret_cast<float2*>(sl + p.Rt * D + 2 * l32) = float2{m * pz, l_tot * pz};
         }
       }
     }
-    if (nsb == 1) return;
+    __syncthreads();  // every wave is done with this stage before it is refilled
   }
-  // Partial state of this split for the reduction pass (a poisoned split
-  // stores NaN so the combined row is NaN as well).
-  const float poison = any_bad ? __builtin_nanf("") : 1.f;
-  const int64_t row = ((int64_t)(b * p.Hq + hq) * p.Lq + i) * p.n_splits + s;
-  float* wa = p.ws_acc + row * D;
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt) {
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * dt + 8 * g4 + 4 * hl;
-      if (D >= 32 || d < D) {
-        *reinterpret_cast<float4*>(wa + d) =
-            float4{acc[dt][4 * g4] * poison, acc[dt][4 * g4 + 1] * poison,
-                   acc[dt][4 * g4 + 2] * poison, acc[dt][4 * g4 + 3] * poison};
-      }
-    }
-  }
-  if (hl == 0) *reinterpret_cast<float2*>(p.ws_ml + 2 * row) = float2{m * poison, l_tot * poison};
+
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  return x;
+// Second pass: combines the pieces of every split sequence. Eight lanes
+// share one (sequence, head group, wave slot, row, 4 columns) item; lane t of
+// the eight combines pieces t, t + 8, ... (all its loads issued together,
+// unconditionally, at addresses clamped to the last piece), then the eight
+// partial states are combined by a fixed butterfly, so the result does not
+// depend on timing. The piece descriptor written by the first pass says
+// where the pieces are.
+constexpr int kMergeLanes = 8;
+constexpr int kMergeBatch = 4;  // pieces per lane per batch
+
+__device__ __forceinline__ void merge_state(float& M, float& L, float4& A, float m2, float l2, float4 a2) {
+  const float Mn = maxf(M, m2);
+  const float wo = rescale_weight(M, Mn), wn = rescale_weight(m2, Mn);
+  L = L * wo + l2 * wn;
+  A.x = A.x * wo + a2.x * wn;
+  A.y = A.y * wo + a2.y * wn;
+  A.z = A.z * wo + a2.z * wn;
+  A.w = A.w * wo + a2.w * wn;
+  M = Mn;
 }
 
-// Combines the split partials of every (sequence, query head, token) row
-// whose sequence spans more than one split. One wave per row.
 template <int DTYPE, int D>
-__global__ __launch_bounds__(64) void paged_reduce_kernel(const PagedParams p) {
+__global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   using E = Elt<DTYPE>;
-  __shared__ float wsh[kPagedReduceChunk];
-  const int row = blockIdx.x;  // (b * Hq + hq) * Lq + i
-  const int i = row % p.Lq;
-  const int bh = row / p.Lq;
-  const int hq = bh % p.Hq, b = bh / p.Hq;
-  const int ctx = p.lens[b];
-  if (ctx < 0 || ctx > p.max_blocks * p.block_size || ctx > p.n_splits * p.split_len ||
-      (ctx > 0 && p.num_blocks < 1))
-    return;  // written as NaN by the main kernel
-  const int nsb = max(1, (ctx + p.split_len - 1) / p.split_len);
-  if (nsb <= 1) return;
-  const int64_t base = (int64_t)row * p.n_splits;
-  const int lane = threadIdx.x;
+  constexpr int Q4 = D / 4;
+  const int t = threadIdx.x % kMergeLanes;
+  int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) / kMergeLanes;
+  const int d4 = (int)(item % Q4);
+  item /= Q4;
+  const int row = (int)(item % p.Rt);
+  item /= p.Rt;
+  const int w = (int)(item % p.NWV);
+  item /= p.NWV;
+  const int gh = (int)(item % p.NG);
+  const int b = (int)(item / p.NG);
+  // Items of one wave belong to at most a few sequences; lanes past the end
+  // or without work still take part in the shuffles below.
+  const bool in = b < p.B;
+  const int4 inf = in ? p.info[(int64_t)gh * p.B + b] : int4{0, 0, 0, 0};
+  const int pieces = inf.y;
+  const int hh = w % p.Hg, qt = w / p.Hg;
+  const int r = qt * 32 + row;
+  const bool act = in && pieces > 1 && r < p.R;
+  const int64_t slot_floats = (int64_t)p.Rt * (D + 2);
 
-  float M = -INFINITY;
-  for (int s = lane; s < nsb; s += 64) M = fmaxf(M, p.ws_ml[2 * (base + s)]);
-  M = wave_max(M);
-  float L = 0.f;
-  for (int s = lane; s < nsb; s += 64) L += rescale_weight(p.ws_ml[2 * (base + s)], M) * p.ws_ml[2 * (base + s) + 1];
-  L = wave_sum(L);
-  const float inv = 1.f / L;
-
-  constexpr int PER = (D + 63) / 64;
-  float acc[PER];
+  float M = -INFINITY, L = 0.f;
+  float4 A = {0.f, 0.f, 0.f, 0.f};
+  if (act) {
+    for (int k0 = t; k0 < pieces; k0 += kMergeLanes * kMergeBatch) {
+      float2 ml[kMergeBatch];
+      float4 a[kMergeBatch];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
-  for (int s0 = 0; s0 < nsb; s0 += kPagedReduceChunk) {
-    const int cnt = min(kPagedReduceChunk, nsb - s0);
-    __syncthreads();
-    for (int j = lane; j < cnt; j += 64) wsh[j] = rescale_weight(p.ws_ml[2 * (base + s0 + j)], M);
-    __syncthreads();
-    const float* src = p.ws_acc + (base + s0) * D;
-    for (int j = 0; j < cnt; ++j) {
-      const float w = wsh[j];
-#pragma unroll
-      for (int q = 0; q < PER; ++q) {
-        const int d = lane + 64 * q;
-        if (D >= 64 || d < D) acc[q] += w * src[(int64_t)j * D + d];
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int k = min(k0 + kMergeLanes * u, pieces - 1);
+        const int side = k == 0 ? inf.z : 0;
+        const float* sl = p.slots + ((((int64_t)(inf.x + k) * p.NG + gh) * 2 + side) * p.NWV + w) * slot_floats;
+        ml[u] = *reinterpret_cast<const float2*>(sl + (int64_t)p.Rt * D + 2 * row);
+        a[u] = *reinterpret_cast<const float4*>(sl + row * D + 4 * d4);
       }
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u)
+        if (k0 + kMergeLanes * u < pieces) merge_state(M, L, A, ml[u].x, ml[u].y, a[u]);
     }
   }
-  uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)i * p.os2;
 #pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    const int d = lane + 64 * q;
-    if (D >= 64 || d < D) orow[d] = (uint16_t)(E::pack2(acc[q] * inv, 0.f) & 0xffffu);
+  for (int off = 1; off < kMergeLanes; off <<= 1) {
+    const float m2 = __shfl_xor(M, off), l2 = __shfl_xor(L, off);
+    const float4 a2 = {__shfl_xor(A.x, off), __shfl_xor(A.y, off), __shfl_xor(A.z, off), __shfl_xor(A.w, off)};
+    // the lower lane of each pair keeps its own state first: same order in both lanes
+    if (t & off) {
+      float Mx = m2, Lx = l2;
+      float4 Ax = a2;
+      merge_state(Mx, Lx, Ax, M, L, A);
+      M = Mx, L = Lx, A = Ax;
+    } else {
+      merge_state(M, L, A, m2, l2, a2);
+    }
   }
+  if (!act || t != 0) return;
+  const int g = r / p.Lq, i = r - g * p.Lq;
+  const int hq = (gh * p.Hg + hh) * p.group + g;
+  const float inv = 1.f / L;
+  uint16_t* orow = p.o + (int64_t)b * p.os0 + hq * p.os1 + (int64_t)i * p.os2;
+  *reinterpret_cast<u32x2*>(orow + 4 * d4) = u32x2{E::pack2(A.x * inv, A.y * inv), E::pack2(A.z * inv, A.w * inv)};
 }
 
-int paged_split_len(int B, int Hk, int n_qt, int max_ctx, int block_size) {
-  // Longest split (<= 512 tokens) that still yields about 1.5k waves at the
-  // longest context; the split's block ids must fit the LDS staging area.
-  const int64_t pairs = (int64_t)B * Hk * n_qt;
-  const int64_t cap = std::max<int64_t>(kPagedTile, (int64_t)(kPagedMaxSplitBlocks - 2) * block_size);
-  int split = 512;
-  while (split > kPagedTile && (split > cap || pairs * ((max_ctx + split - 1) / split) < 1536)) split /= 2;
-  return split;
+PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size) {
+  PagedGeom g{};
+  g.ok = 0;
+  if (B < 1 || Hq < 1 || Hk < 1 || Lq < 1 || Hq % Hk || block_size < 1 || ctx_limit < 0 ||
+      !(D == 16 || D == 32 || D == 64 || D == 128 || D == 256)) {
+    g.err = "invalid shape";
+    return g;
+  }
+  g.R = (Hq / Hk) * Lq;
+  g.n_qt = (g.R + 31) / 32;
+  g.Rt = std::min(32, g.R);
+  if (g.n_qt > kPagedMaxWaves) {
+    g.err = "more than 256 query rows per kv head (num_heads / num_kv_heads * new tokens)";
+    return g;
+  }
+  g.Hg = 1;
+  for (int h = 1; h <= Hk; ++h)
+    if (Hk % h == 0 && h * D <= 512 && h * g.n_qt <= kPagedMaxWaves) g.Hg = h;
+  g.NG = Hk / g.Hg;
+  g.NWV = g.Hg * g.n_qt;
+  g.NCH = g.Hg * D / 8;
+  const size_t stage = (size_t)2 * kPagedTile * g.NCH * 16;  // K and V tiles
+  const int dpw = D / 16;
+  int nst = (int)std::min<size_t>(4, kPagedLdsBudget / stage);
+  nst = std::min(std::max(nst, 2), 1 + 31 / dpw);  // 2 * dpw * (nst - 1) copies fit vmcnt
+  g.NST = nst;
+  g.lds_bytes = (size_t)nst * stage;
+  const size_t static_lds = sizeof(int32_t) * (kPagedIds + 8 * kPagedEntries) + 16;
+  int wpc = (int)((160 * 1024) / (g.lds_bytes + static_lds));
+  wpc = std::max(1, std::min(wpc, 16 / g.NWV));
+  const int64_t nt_upper = (int64_t)B * ((ctx_limit + kPagedTile - 1) / kPagedTile);
+  const int ids_per_tile = (kPagedTile + block_size - 1) / block_size + 2;
+  const int tcap = std::min(kPagedEntries, kPagedIds / ids_per_tile);
+  int64_t wg = std::max<int64_t>(1, (int64_t)kPagedCUs * wpc / g.NG);
+  wg = std::min<int64_t>(wg, std::max<int64_t>(1, nt_upper));
+  wg = std::max<int64_t>(wg, (nt_upper + tcap - 1) / tcap);
+  if (wg * g.NG > INT_MAX) {
+    g.err = "problem too large for one launch";
+    return g;
+  }
+  g.Wg = (int)wg;
+  g.info_bytes = ((size_t)g.NG * B * sizeof(int4) + 255) / 256 * 256;
+  g.slot_bytes = (size_t)g.NG * g.Wg * 2 * g.NWV * g.Rt * (D + 2) * sizeof(float);
+  g.ok = 1;
+  return g;
 }
 
 template <int DTYPE, int D>
-static hipError_t launch_paged_t(const PagedParams& p, hipStream_t stream) {
-  const int64_t n_wg = (int64_t)p.B * p.n_splits * p.n_qt * p.Hk;
-  hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D>), dim3((unsigned)n_wg), dim3(64), 0, stream, p);
+static hipError_t launch_paged_t(const PagedParams& p, size_t lds, hipStream_t stream) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kPagedLdsBudget);
+  });
+  if (attr != hipSuccess) return attr;
+  const int64_t n_wg = (int64_t)p.NG * p.Wg;
+  hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.n_splits <= 1) return e;
-  hipLaunchKernelGGL((paged_reduce_kernel<DTYPE, D>), dim3(p.B * p.Hq * p.Lq), dim3(64), 0, stream, p);
+  if (e != hipSuccess) return e;
+  const int64_t threads = (int64_t)p.B * p.NG * p.NWV * p.Rt * (D / 4) * kMergeLanes;
+  hipLaunchKernelGGL((paged_merge_kernel<DTYPE, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 template <int DTYPE>
-static hipError_t launch_paged_d(const PagedParams& p, int D, hipStream_t stream) {
+static hipError_t launch_paged_d(const PagedParams& p, int D, size_t lds, hipStream_t stream) {
   switch (D) {
-    case 16: return launch_paged_t<DTYPE, 16>(p, stream);
-    case 32: return launch_paged_t<DTYPE, 32>(p, stream);
-    case 64: return launch_paged_t<DTYPE, 64>(p, stream);
-    case 128: return launch_paged_t<DTYPE, 128>(p, stream);
-    case 256: return launch_paged_t<DTYPE, 256>(p, stream);
+    case 16: return launch_paged_t<DTYPE, 16>(p, lds, stream);
+    case 32: return launch_paged_t<DTYPE, 32>(p, lds, stream);
+    case 64: return launch_paged_t<DTYPE, 64>(p, lds, stream);
+    case 128: return launch_paged_t<DTYPE, 128>(p, lds, stream);
+    case 256: return launch_paged_t<DTYPE, 256>(p, lds, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_paged(const PagedParams& p, int dtype, int D, hipStream_t stream) {
-  return dtype == 0 ? launch_paged_d<0>(p, D, stream) : launch_paged_d<1>(p, D, stream);
+hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds, hipStream_t stream) {
+  return dtype == 0 ? launch_paged_d<0>(p, D, lds, stream) : launch_paged_d<1>(p, D, lds, stream);
 }
 
 }  // namespace cie

@@ -96,9 +96,24 @@ def flash_attention(
 def paged_workspace_bytes(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size: int,
                           max_blocks_per_seq: int, max_context: int | None = None) -> int:
     """Device workspace (bytes) a :func:`paged_attention` call of this shape
-    needs for its context-split partials."""
+    needs: per-sequence piece descriptors and the partial states of
+    sequences split across workgroups."""
     return int(_lib.load().cie_paged_workspace_bytes(
         B, Hq, Hk, Lq, D, int(max_context or 0), block_size, max_blocks_per_seq))
+
+
+# Workspaces, one per (device, stream): calls on one stream run in order, so
+# they can share it.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _cached_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def paged_attention(
@@ -121,9 +136,12 @@ def paged_attention(
     context_lens: int32 (B,), tokens in the pool per sequence including the
     Lq new ones (the reference appends before attending). With ``causal``
     new token i sees positions <= context_len - Lq + i. ``max_context`` (an
-    upper bound of context_lens) lets the launch size its context splits
-    tighter than max_blocks * block_size. Equal to ``flash_attention`` over
-    ``cache.gather`` per sequence. Returns (B, Hq, Lq, D) in q's dtype.
+    upper bound of context_lens; a longer context yields NaN) lets the launch
+    size its work split tighter than max_blocks * block_size. ``workspace``:
+    a caller-owned uint8 device buffer of at least
+    :func:`paged_workspace_bytes` bytes; by default a cached per-(device,
+    stream) buffer is used. Equal to ``flash_attention`` over ``cache.gather``
+    per sequence. Returns (B, Hq, Lq, D) in q's dtype.
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_tables", block_tables), ("context_lens", context_lens)):
@@ -157,17 +175,21 @@ def paged_attention(
     k_cache, v_cache = _kernel_layout(k_cache), _kernel_layout(v_cache)
     mc = int(max_context or 0)
     ws_bytes = int(lib.cie_paged_workspace_bytes(B, Hq, Hk, Lq, D, mc, block_size, max_blocks))
-    if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    stream = _lib.stream_handle(q.device)
+    if workspace is None:
+        workspace = _cached_workspace(q.device, stream, ws_bytes)
+    elif not workspace.is_cuda or workspace.device != q.device:
+        raise RuntimeError("paged_attention: workspace must be on the query's CUDA device")
+    ws_have = workspace.numel() * workspace.element_size()
     out = torch.empty((B, Hq, Lq, D), dtype=q.dtype, device=q.device)
     with torch.cuda.device(q.device):
         rc = lib.cie_paged_fwd(
             q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(),
             out.data_ptr(),
-            workspace.data_ptr() if ws_bytes else None,
-            ws_bytes,
+            workspace.data_ptr(),
+            ws_have,
             _lib.strides(q), _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out),
             B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc,
-            float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype], _lib.stream_handle(q.device))
+            float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype], stream)
     _lib.check(rc)
     return out

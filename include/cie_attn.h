@@ -73,7 +73,10 @@ int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
                   float scale, int causal, int dtype, void* stream);
 
 /*
- * Bytes of device workspace cie_paged_fwd needs for this shape (may be 0).
+ * Bytes of device workspace cie_paged_fwd needs for this shape (0 for an
+ * unsupported shape): per-sequence piece descriptors and the partial states
+ * of sequences split across workgroups. Any contents; calls that run
+ * concurrently must not share a workspace.
  * max_context bounds every context_lens[b]; pass <= 0 to use the table bound
  * max_blocks_per_seq * block_size (the value cie_paged_fwd uses the same way).
  * No reference counterpart: the reference never splits a context.
@@ -97,8 +100,11 @@ size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D,
  *   o: (B, Hq, Lq, D)
  * Equals flash_attention_ref(q[b], gather(b), causal, scale) per sequence.
  * A block id outside [0, num_blocks) or a context length outside
- * [0, max_blocks_per_seq * block_size] is never dereferenced: the affected
- * sequence's output is written as NaN instead.
+ * [0, min(max_context, max_blocks_per_seq * block_size)] is never
+ * dereferenced: the affected sequence's output is written as NaN instead.
+ * (Hq / Hk) * Lq must be at most 256. workspace: at least
+ * cie_paged_workspace_bytes bytes, 16-byte aligned. Two kernels are launched
+ * on the stream: the main pass and the merge of split sequences.
  */
 int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* block_tables, const int32_t* context_lens,
