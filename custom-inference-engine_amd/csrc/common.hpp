@@ -185,6 +185,19 @@ __device__ __forceinline__ void dma16_at(const void* gptr, uint32_t lds_addr) {
   lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
 }
+// Scalar-base form: lane l loads sbase + voff (voff a 32-bit byte offset),
+// no per-lane 64-bit address arithmetic. sbase must be wave-uniform.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t a = (uint64_t)(size_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (const void*)(size_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_addr)
+               : "memory", "m0");
+}
 // 4-byte variant: lane l's dword lands at LDS byte address lds_addr + 4 * l.
 __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_addr) {
   lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);

@@ -126,14 +126,35 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     lrow[j] = P / C::S;
     lchk[j] = 8 * ((P % C::S) ^ chunk_swizzle<C::S>(lrow[j]));
   }
+  // Byte offsets of this lane's chunks from the first key of a tile; full
+  // tiles add them to a scalar tile base (no per-lane address math), the
+  // key-tail tile clamps rows to the last key.
+  const bool off32 = (int64_t)BN * max(p.ks2, p.vs2) * 2 + 2 * D < ((int64_t)1 << 31);
+  uint32_t koff[C::NW], voff[C::NW];
+#pragma unroll
+  for (int j = 0; j < C::NW; ++j) {
+    koff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.ks2 + lchk[j])) : 0u;
+    voff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.vs2 + lchk[j])) : 0u;
+  }
+  const uint32_t ring_lds = lds_addr_of(ring);
   auto issue = [&](int t) {
     const int n0 = t * BN;
-    uint16_t* st = ring + (t % C::NST) * C::STAGE + wave * C::NW * 512;
+    const uint32_t st = ring_lds + 2u * (uint32_t)((t % C::NST) * C::STAGE + wave * C::NW * 512);
+    if (off32 && n0 + BN <= p.Lk) {
+      const void* kt = uniform_ptr(kb + (int64_t)n0 * p.ks2);
+      const void* vt = uniform_ptr(vb + (int64_t)n0 * p.vs2);
 #pragma unroll
-    for (int j = 0; j < C::NW; ++j) {
-      const int key = min(n0 + lrow[j], last_key);
-      dma16(kb + (int64_t)key * p.ks2 + lchk[j], st + 512 * j);
-      dma16(vb + (int64_t)key * p.vs2 + lchk[j], st + C::TILE + 512 * j);
+      for (int j = 0; j < C::NW; ++j) {
+        dma16_sv(kt, koff[j], st + 1024u * j);
+        dma16_sv(vt, voff[j], st + 2u * C::TILE + 1024u * j);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::NW; ++j) {
+        const int key = min(n0 + lrow[j], last_key);
+        dma16_at(kb + (int64_t)key * p.ks2 + lchk[j], st + 1024u * j);
+        dma16_at(vb + (int64_t)key * p.vs2 + lchk[j], st + 2u * C::TILE + 1024u * j);
+      }
     }
   };
 
@@ -198,13 +219,16 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     mx = rowmax(sc);
   }
   const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
-  for (int t = 0; t < n_tiles; ++t) {
+  // One pipeline step: sc holds S(t), S(t+1) is produced in sn. The loop
+  // below runs it twice per trip with the two score arrays swapped, so the
+  // scores are never copied between registers.
+  auto step = [&](const int t, f32x16* sc, f32x16* sn) {
     if (t + 1 < n_tiles) {
       wait_ahead<C::NST, C::PER_TILE>(min(C::NST - 3, n_tiles - 2 - t));
       __syncthreads();  // tile t+1 resident for all waves; stage of tile t-1 free
       if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
     }
-    if (t * BN >= wave_kend) continue;  // wave-uniform: every row of the wave is done
+    if (t * BN >= wave_kend) return;  // wave-uniform: every row of the wave is done
 
     // lazy rescale against the row max of S(t)
     const float mxs = xhalf_max(mx) * c;
@@ -226,7 +250,6 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // last tile the stage read is stale and S(t+1) is discarded. The empty
     // volatile asm consumes each packed pair inside its chunk; without it the
     // softmax would be sunk next to the P.V MFMAs that use it.
-    f32x16 sn[C::MT];
     u32x4 pb[2 * C::MT];
     {
       const uint16_t* ks = ring + ((t + 1) % C::NST) * C::STAGE;
@@ -293,8 +316,11 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
         }
       }
     }
-#pragma unroll
-    for (int mt2 = 0; mt2 < C::MT; ++mt2) sc[mt2] = sn[mt2];
+  };
+  f32x16 sb[C::MT];
+  for (int t = 0; t < n_tiles; t += 2) {
+    step(t, sc, sb);
+    if (t + 1 < n_tiles) step(t + 1, sb, sc);
   }
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
