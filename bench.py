@@ -16,7 +16,9 @@ The same line carries
   extra         the other workloads: paged decode (B=32, fp16) and speculative
                 verify (B=8, Lq=5, bf16) in GB/s against the 8 TB/s HBM peak,
                 timed while rotating over >= 512 MiB of KV pool copies so the
-                256 MiB Infinity Cache cannot hold them, and the S=16384
+                256 MiB Infinity Cache cannot hold them; the paged KV append
+                of a prefill (4 x 2048 tokens) and of a decode step (32 x 1
+                token) in GB/s of bytes read + written; and the S=16384
                 D=128 bf16 prefill in TFLOP/s.
 """
 
@@ -150,6 +152,55 @@ class PagedLaunch:
             _lib.check(rc)
 
 
+class AppendLaunch:
+    """Pre-bound cie_kv_append: B sequences x L new tokens (Hk=8, D=64, fp16,
+    block_size 16) into a pool whose blocks are a random permutation, rotating
+    over copies of the sources and pools that together exceed `min_bytes` so
+    the Infinity Cache cannot hold them."""
+
+    def __init__(self, B, L, dev, seed=6, min_bytes=512 << 20):
+        import torch
+        from engine import _lib
+
+        self.lib = _lib.load()
+        g = torch.Generator().manual_seed(seed)
+        Hk, D, bs = 8, 64, 16
+        starts = torch.randint(0, 4096, (B,), generator=g, dtype=torch.int32)
+        need = [-(-(int(s) + L) // bs) for s in starts]
+        nb = sum(need)
+        perm = torch.randperm(nb, generator=g).to(torch.int32)
+        width = max(need)
+        bt = torch.zeros(B, width, dtype=torch.int32)
+        pos = 0
+        for b, n in enumerate(need):
+            bt[b, :n] = perm[pos:pos + n]
+            pos += n
+        T = B * L
+        k = torch.randn(T, Hk, D, generator=g).half()
+        v = torch.randn(T, Hk, D, generator=g).half()
+        per_copy = 2 * T * Hk * D * 2 + 2 * nb * bs * Hk * D * 2
+        self.copies = max(1, -(-min_bytes // per_copy))
+        self.bufs = []
+        for _ in range(self.copies):
+            kc = torch.zeros(nb, bs, Hk, D, dtype=torch.float16, device=dev)
+            self.bufs.append((k.to(dev), v.to(dev), kc, torch.zeros_like(kc)))
+        self.bt = bt.to(dev)
+        self.cu = torch.arange(0, T + 1, L, dtype=torch.int32).to(dev)
+        self.st = starts.to(dev)
+        k0, v0, kc0, vc0 = self.bufs[0]
+        self._keep = [_lib.strides3(k0), _lib.strides3(v0), _lib.strides(kc0), _lib.strides(vc0)]
+        self.ptrs = [tuple(t.data_ptr() for t in bufs) for bufs in self.bufs]
+        self.tail = (*self._keep, self.bt.data_ptr(), self.cu.data_ptr(), self.st.data_ptr(), None,
+                     B, T, L, Hk, D, nb, bs, width, 0, _lib.stream_handle(dev))
+        self.bytes = 2 * 2 * T * Hk * D * 2  # K and V rows, read once and written once
+
+    def __call__(self, i=0):
+        rc = self.lib.cie_kv_append(*self.ptrs[i % self.copies], *self.tail)
+        if rc:
+            from engine import _lib
+            _lib.check(rc)
+
+
 def event_time_ms(fn, n, warmup, trials=3):
     """Median over trials of (HIP-event time of n back-to-back launches) / n."""
     import torch
@@ -241,6 +292,13 @@ def main():
                            "bytes": int(c.bytes), "pool_copies": pl.copies,
                            "dtype": "fp16" if c.q.dtype == torch.float16 else "bf16"}
             del pl
+        for name, (B, L) in (("append_prefill_b4_l2048", (4, 2048)), ("append_decode_b32", (32, 1))):
+            al = AppendLaunch(B, L, dev)
+            ms = event_time_ms(al, max(50, 4 * al.copies), al.copies)
+            gbs = al.bytes / (ms / 1e3) / 1e9
+            extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
+                           "bytes": int(al.bytes), "copies": al.copies, "dtype": "fp16"}
+            del al
         c5 = workloads.prefill_s16384()
         f5 = FlashLaunch(c5, dev)
         ms = event_time_ms(f5, 5, 1)

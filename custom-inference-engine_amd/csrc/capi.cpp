@@ -231,4 +231,64 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   return launch_status(cie::launch_paged(p, dtype, D, g.lds_bytes, static_cast<hipStream_t>(stream)));
 }
 
+int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                  const int64_t* new_stride, const int64_t* v_new_stride,
+                  const int64_t* kc_stride, const int64_t* vc_stride,
+                  const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
+                  uint32_t* status, int B, int T, int max_new, int Hk, int D,
+                  int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream) {
+  if (dtype != CIE_DTYPE_F16 && dtype != CIE_DTYPE_BF16)
+    return fail(CIE_EDTYPE, "unsupported dtype code %d (f16 = 0, bf16 = 1)", dtype);
+  if (!head_dim_ok(D)) return fail(CIE_EHEADDIM, "head_dim must be a power of 2 in [16, 256], got %d", D);
+  if (B < 0 || T < 0 || max_new < 0 || Hk < 1)
+    return fail(CIE_EINVAL, "invalid sizes (B=%d, T=%d, max_new=%d, Hk=%d)", B, T, max_new, Hk);
+  if (block_size < 1 || num_blocks < 0 || max_blocks_per_seq < 0)
+    return fail(CIE_EINVAL, "invalid pool geometry (num_blocks=%d, block_size=%d, max_blocks_per_seq=%d)",
+                num_blocks, block_size, max_blocks_per_seq);
+  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff)
+    return fail(CIE_EINVAL, "max_blocks_per_seq * block_size exceeds 2^31");
+  if ((int64_t)max_new * Hk * D / 8 >= ((int64_t)1 << 31)) return fail(CIE_EINVAL, "too many new tokens for one launch");
+  if (B == 0 || T == 0 || max_new == 0) {
+    g_err.clear();
+    return CIE_OK;
+  }
+  CIE_TRY(check_ptr("k_new", k_new));
+  CIE_TRY(check_ptr("v_new", v_new));
+  CIE_TRY(check_ptr("k_cache", k_cache));
+  CIE_TRY(check_ptr("v_cache", v_cache));
+  if (!block_tables || !cu_new || !start) return fail(CIE_EINVAL, "block_tables / cu_new / start: NULL pointer");
+  // (T, Hk, D) sources: reuse the 4-d stride check on (1, T, Hk, D)
+  const int64_t ns[4] = {0, new_stride ? new_stride[0] : 0, new_stride ? new_stride[1] : 0,
+                         new_stride ? new_stride[2] : 0};
+  const int64_t ms[4] = {0, v_new_stride ? v_new_stride[0] : 0, v_new_stride ? v_new_stride[1] : 0,
+                         v_new_stride ? v_new_stride[2] : 0};
+  if (!new_stride || !v_new_stride) return fail(CIE_EINVAL, "k_new / v_new: stride array is NULL");
+  CIE_TRY(check_strides("k_new", ns));
+  CIE_TRY(check_strides("v_new", ms));
+  CIE_TRY(check_strides("k_cache", kc_stride));
+  CIE_TRY(check_strides("v_cache", vc_stride));
+
+  cie::AppendParams p{};
+  p.k_new = static_cast<const uint16_t*>(k_new);
+  p.v_new = static_cast<const uint16_t*>(v_new);
+  p.kc = static_cast<uint16_t*>(k_cache);
+  p.vc = static_cast<uint16_t*>(v_cache);
+  p.bt = block_tables;
+  p.cu_new = cu_new;
+  p.start = start;
+  p.status = status;
+  p.ns0 = ns[1]; p.ns1 = ns[2];
+  p.ms0 = ms[1]; p.ms1 = ms[2];
+  p.ks0 = kc_stride[0]; p.ks1 = kc_stride[1]; p.ks2 = kc_stride[2];
+  p.vs0 = vc_stride[0]; p.vs1 = vc_stride[1]; p.vs2 = vc_stride[2];
+  p.num_blocks = num_blocks;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_size = block_size;
+  p.cpr = (uint32_t)(Hk * D / 8);
+  p.lg_cph = (uint32_t)__builtin_ctz((unsigned)(D / 8));
+  p.cprdiv = cie::make_fastdiv(p.cpr);
+  p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
+  return launch_status(cie::launch_kv_append(p, B, max_new, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

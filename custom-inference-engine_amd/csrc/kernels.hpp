@@ -82,7 +82,28 @@ struct PagedGeom {
 };
 PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size);
 
+// Paged KV append: new token rows (T, Hk, D) into the pool through block tables.
+struct AppendParams {
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int32_t* bt;      // [B][max_blocks]
+  const int32_t* cu_new;  // [B + 1] prefix offsets of each sequence's rows in k_new / v_new
+  const int32_t* start;   // [B] position of each sequence's first new token
+  uint32_t* status;       // optional: set to 1 when a position or block id is out of range
+  int64_t ns0, ns1;       // k_new strides (token, head); head_dim stride 1
+  int64_t ms0, ms1;       // v_new strides
+  int64_t ks0, ks1, ks2;  // k pool strides (block, offset, head)
+  int64_t vs0, vs1, vs2;
+  int num_blocks, max_blocks, block_size;
+  uint32_t cpr;           // 16-byte chunks per token row (Hk * D / 8)
+  uint32_t lg_cph;        // log2 of chunks per head row (D / 8)
+  FastDiv cprdiv, bsdiv;
+};
+
 hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stream);
+hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, hipStream_t stream);
 hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, hipStream_t stream);
 
 }  // namespace cie

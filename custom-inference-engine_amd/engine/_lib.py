@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "cie_flash_fwd",
     "cie_paged_workspace_bytes",
     "cie_paged_fwd",
+    "cie_kv_append",
 )
 
 
@@ -63,6 +64,9 @@ def _declare(lib: ctypes.CDLL) -> None:
                                   _i, _i, _i, _i, _i, _i, _i, _i, _i,
                                   ctypes.c_float, _i, _i, _vp]
     lib.cie_paged_fwd.restype = _i
+    lib.cie_kv_append.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
+                                  _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]
+    lib.cie_kv_append.restype = _i
 
 
 def load() -> ctypes.CDLL:
@@ -103,6 +107,12 @@ def strides(t: torch.Tensor) -> ctypes.Array:
     multiplied by a non-zero index, so it is passed as 0."""
     st = [0 if t.shape[i] == 1 else t.stride(i) for i in range(3)] + [t.stride(3)]
     return (ctypes.c_int64 * 4)(*st)
+
+
+def strides3(t: torch.Tensor) -> ctypes.Array:
+    """Element strides of a (T, Hk, D) tensor (size-1 dimensions as 0)."""
+    st = [0 if t.shape[i] == 1 else t.stride(i) for i in range(2)] + [t.stride(2)]
+    return (ctypes.c_int64 * 3)(*st)
 
 
 def stream_handle(device: torch.device) -> int:

@@ -11,10 +11,15 @@ API and pool layout follow the reference's ``engine/cache/kv_cache.py``:
   ``append`` (:102-139), ``gather`` (:141-165), ``fork`` (:169-185),
   ``rollback`` (:187-194), ``stats`` (:196-210).
 
-Added for the paged kernel: :func:`block_table_tensor`, which packs host
-block tables into the int32 ``(B, max_blocks)`` / ``(B,)`` device format
-``paged_attention`` reads, and :meth:`PagedKVCache.attend`, which runs it on
-one layer's pools.
+Added for the paged kernels: :func:`block_table_tensor`, which packs host
+block tables into the int32 ``(B, max_blocks)`` / ``(B,)`` device format the
+kernels read; :func:`kv_append`, the batched device write of new tokens
+(``cie_kv_append``); :meth:`PagedKVCache.append_batch`, its per-layer use for
+many sequences; and :meth:`PagedKVCache.attend`, which runs
+``paged_attention`` on one layer's pools. On a CUDA device ``append`` writes
+through ``cie_kv_append`` (the reference's per-block slice loop,
+kv_cache.py:128-136, becomes one launch); a cache on the CPU device keeps the
+reference's slice copies, since no kernel runs there.
 """
 
 from __future__ import annotations
@@ -63,6 +68,54 @@ def block_table_tensor(
             bt[i, :len(t.blocks)] = torch.tensor(t.blocks, dtype=torch.int32)
     lens = torch.tensor([t.length for t in tables], dtype=torch.int32)
     return bt.to(device), lens.to(device)
+
+
+def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+              block_tables: torch.Tensor, cu_new: torch.Tensor, start: torch.Tensor,
+              max_new: int, status: torch.Tensor | None = None) -> None:
+    """Write new tokens of B sequences into one layer's pools on the GPU.
+
+    k_new / v_new: (T, Hk, D); the rows of sequence b are
+    ``cu_new[b] .. cu_new[b+1]-1`` (int32 (B+1,), device) and go to positions
+    ``start[b] + i`` (int32 (B,), device) through ``block_tables`` (int32
+    (B, max_blocks), device, already holding the needed blocks). ``max_new``
+    bounds the per-sequence count. ``status`` (optional int32/uint32 (1,),
+    device) is set to 1 if a position or block id was out of range; those
+    tokens are not written.
+    """
+    from engine import _lib
+
+    for name, t in (("k_new", k_new), ("v_new", v_new), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("block_tables", block_tables), ("cu_new", cu_new), ("start", start)):
+        if not t.is_cuda or t.device != k_cache.device:
+            raise RuntimeError(f"kv_append requires CUDA tensors on one device ({name})")
+    if k_new.dtype != k_cache.dtype or v_new.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise ValueError("kv_append: new tokens and pools must share a dtype")
+    if k_new.dim() != 3 or tuple(v_new.shape) != tuple(k_new.shape):
+        raise ValueError(f"kv_append expects k_new, v_new of shape (T, Hk, D), got {tuple(k_new.shape)}, "
+                         f"{tuple(v_new.shape)}")
+    nb, bs, Hk, D = k_cache.shape
+    if tuple(v_cache.shape) != tuple(k_cache.shape) or k_new.shape[1:] != (Hk, D):
+        raise ValueError(f"kv_append: pool {tuple(k_cache.shape)} does not match tokens {tuple(k_new.shape)}")
+    if k_cache.dtype not in _lib.DTYPE_CODES:
+        raise ValueError(f"attention kernels expect FP16 or BF16 Q/K/V, got {k_cache.dtype}")
+    B = start.shape[0]
+    bt = block_tables.to(torch.int32).contiguous()
+    cu = cu_new.to(torch.int32).contiguous()
+    st = start.to(torch.int32).contiguous()
+    if bt.dim() != 2 or bt.shape[0] != B or cu.shape[0] != B + 1:
+        raise ValueError("kv_append: block_tables must be (B, max_blocks) and cu_new (B + 1,)")
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1:
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(k_cache.device):
+        rc = lib.cie_kv_append(
+            k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            _lib.strides3(k_new), _lib.strides3(v_new), _lib.strides(k_cache), _lib.strides(v_cache),
+            bt.data_ptr(), cu.data_ptr(), st.data_ptr(), status.data_ptr() if status is not None else None,
+            B, k_new.shape[0], int(max_new), Hk, D, nb, bs, bt.shape[1],
+            _lib.DTYPE_CODES[k_cache.dtype], _lib.stream_handle(k_cache.device))
+    _lib.check(rc)
 
 
 class PagedKVCache:
@@ -134,15 +187,53 @@ class PagedKVCache:
         end = start + L
         while len(table.blocks) < table.num_blocks_needed(end):
             table.blocks.append(self._alloc_block())
-        bs = self.cfg.block_size
-        done = 0
-        while done < L:
-            bid, off = table.logical_to_physical(start + done)
-            n = min(bs - off, L - done)
-            self.k[layer][bid, off:off + n] = k[done:done + n]
-            self.v[layer][bid, off:off + n] = v[done:done + n]
-            done += n
+        if L and self.device.type == "cuda":
+            # one launch; block ids, row offsets and start travel in one small copy
+            first = start // self.cfg.block_size
+            ids = table.blocks[first:table.num_blocks_needed(end)]
+            meta = torch.tensor(ids + [0, L, start % self.cfg.block_size], dtype=torch.int32).to(self.device)
+            n = len(ids)
+            kv_append(k, v, self.k[layer], self.v[layer], meta[:n].view(1, n), meta[n:n + 2], meta[n + 2:n + 3],
+                      max_new=L)
+        elif L:
+            bs = self.cfg.block_size
+            done = 0
+            while done < L:
+                bid, off = table.logical_to_physical(start + done)
+                n = min(bs - off, L - done)
+                self.k[layer][bid, off:off + n] = k[done:done + n]
+                self.v[layer][bid, off:off + n] = v[done:done + n]
+                done += n
         table.length = max(table.length, end)
+
+    def append_batch(self, layer: int, tables: Sequence[BlockTable], k: torch.Tensor, v: torch.Tensor,
+                     lengths: Sequence[int], starts: Sequence[int] | None = None,
+                     block_tables: torch.Tensor | None = None) -> None:
+        """``append`` for many sequences in one launch: k, v are (T, Hk, D)
+        with the rows of ``tables[b]`` consecutive (``lengths[b]`` of them),
+        written at ``starts[b]`` (default: each table's end). Blocks are
+        allocated on the host first; ``block_tables`` (the device table of
+        ``block_table_tensor``, e.g. shared by all layers of a step) is built
+        when not given."""
+        self._validate(k)
+        self._validate(v)
+        if self.device.type != "cuda":
+            raise RuntimeError("append_batch requires a CUDA cache")
+        starts = [t.length for t in tables] if starts is None else list(starts)
+        for t, s0, n in zip(tables, starts, lengths):
+            while len(t.blocks) < t.num_blocks_needed(s0 + n):
+                t.blocks.append(self._alloc_block())
+        if block_tables is None:
+            block_tables, _ = block_table_tensor(tables, self.device)
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        meta = torch.tensor(cu + starts, dtype=torch.int32).to(self.device)
+        B = len(tables)
+        kv_append(k, v, self.k[layer], self.v[layer], block_tables, meta[:B + 1], meta[B + 1:],
+                  max_new=max(list(lengths) + [0]))
+        for t, s0, n in zip(tables, starts, lengths):
+            t.length = max(t.length, s0 + n)
 
     def gather(self, layer: int, table: BlockTable) -> tuple[torch.Tensor, torch.Tensor]:
         """Dense (L, Hk, D) copies of one sequence's K and V history."""

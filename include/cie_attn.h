@@ -116,6 +116,31 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
                   int max_context, float scale, int causal, int dtype,
                   void* stream);
 
+/*
+ * Paged KV append: writes the new tokens of B sequences into the pool.
+ *   k_new, v_new: (T, Hk, D) rows; the rows of sequence b are
+ *        cu_new[b] .. cu_new[b+1]-1 (int32 [B+1], cu_new[0] = 0, cu_new[B] = T)
+ *   new_stride / v_new_stride: element strides of (T, Hk, D) (last must be 1)
+ *   k_cache, v_cache: (num_blocks, block_size, Hk, D) pools as in cie_paged_fwd
+ *   block_tables: int32 [B, max_blocks_per_seq] (already holding the blocks the
+ *        new tokens need); start: int32 [B], position of each sequence's first
+ *        new token; token i of sequence b goes to position start[b] + i
+ *   max_new: an upper bound of cu_new[b+1] - cu_new[b] (sizes the launch)
+ *   status: optional uint32 on the device, set to 1 when a position falls
+ *        outside the table or a block id outside [0, num_blocks) (such tokens
+ *        are not written); may be NULL
+ * Reference: the per-block slice loop of PagedKVCache.append,
+ * engine/cache/kv_cache.py:128-136 (block allocation, :122-125, stays on the
+ * host), with the block ids read on the device instead of copied per call
+ * (kv_cache.py:154).
+ */
+int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                  const int64_t* new_stride, const int64_t* v_new_stride,
+                  const int64_t* kc_stride, const int64_t* vc_stride,
+                  const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
+                  uint32_t* status, int B, int T, int max_new, int Hk, int D,
+                  int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,7 +11,8 @@ Contents
 ``attention_ref``  fp32 torch restatement of the reference's
                    ``kernels/ref/flash_attention_ref.py:8-56`` plus the paged
                    composition (``engine/cache/kv_cache.py:141-165`` gather,
-                   ``engine/cache/block_table.py:23-26`` block math).
+                   ``engine/cache/block_table.py:23-26`` block math) and the
+                   append loop (``engine/cache/kv_cache.py:128-136``).
 ``brute``          fp64 numpy brute force written independently of the
                    above (explicit per-row max-subtracted exponentials).
 
@@ -24,6 +25,7 @@ mistakes that those checks must catch. No function is "parity unpinned".
 """
 
 from oracle.attention_ref import (  # noqa: F401
+    append_ref,
     attention_rows_ref,
     flash_attention_ref,
     flash_attention_ref_chunked,

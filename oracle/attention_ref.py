@@ -186,3 +186,23 @@ def paged_attention_ref(
         vd = gather_ref(v_pool, bt[b], L).float().transpose(0, 1).unsqueeze(0)
         out[b] = flash_attention_ref_chunked(q[b:b + 1].cpu(), kd, vd, causal=causal, scale=scale)[0]
     return out
+
+
+def append_ref(k_pool: torch.Tensor, v_pool: torch.Tensor, blocks, start: int, k: torch.Tensor,
+               v: torch.Tensor) -> None:
+    """In-place write of ``k``, ``v`` (L, Hk, D) at positions start..start+L-1
+    of the sequence whose physical blocks are ``blocks``; the slice loop of
+    ``engine/cache/kv_cache.py:128-136`` (one slice assignment per block
+    spanned, ``take = min(bs - off, L - src_off)``). Block allocation
+    (``:122-125``) is the caller's: ``blocks`` must already cover the range."""
+    bs = k_pool.shape[1]
+    L = k.shape[0]
+    src = 0
+    pos = start
+    while src < L:
+        bid, off = logical_to_physical_ref(blocks, bs, pos)
+        take = min(bs - off, L - src)
+        k_pool[bid, off:off + take] = k[src:src + take]
+        v_pool[bid, off:off + take] = v[src:src + take]
+        pos += take
+        src += take

@@ -314,3 +314,44 @@ def test_paged_ref_invariant_to_block_relabelling():
     vp2[relabel] = vp
     bt2 = relabel[bt.long()].int()
     _same(paged_attention_ref(q, kp2, vp2, bt2, lens), base, 0)
+
+
+# ---------------------------------------------------------------- append
+
+def test_append_ref_round_trips_through_gather_and_spans_blocks():
+    from oracle import append_ref
+
+    g = torch.Generator().manual_seed(31)
+    bs, Hk, D = 4, 2, 16
+    kp = torch.zeros(9, bs, Hk, D)
+    vp = torch.zeros(9, bs, Hk, D)
+    blocks = [7, 2, 5, 0]
+    k = torch.randn(11, Hk, D, generator=g)
+    v = torch.randn(11, Hk, D, generator=g)
+    append_ref(kp, vp, blocks, 3, k, v)  # starts mid-block, spans 4 blocks
+    assert torch.equal(gather_ref(kp, blocks, 14)[3:], k)
+    assert torch.equal(gather_ref(vp, blocks, 14)[3:], v)
+    # positions before start untouched, blocks outside the table untouched
+    assert (gather_ref(kp, blocks, 3) == 0).all()
+    assert (kp[[1, 3, 4, 6, 8]] == 0).all()
+    # every element lands where logical_to_physical says (independent form)
+    for t in range(11):
+        bid, off = blocks[(3 + t) // bs], (3 + t) % bs
+        assert torch.equal(kp[bid, off], k[t]) and torch.equal(vp[bid, off], v[t])
+
+
+def test_append_ref_explicit_start_overwrites():
+    # the reference's "append at start < length rewrites" behaviour (tests/cache/test_kv_cache.py:52-77)
+    from oracle import append_ref
+
+    bs, Hk, D = 4, 1, 16
+    kp = torch.zeros(3, bs, Hk, D)
+    vp = torch.zeros(3, bs, Hk, D)
+    blocks = [2, 0]
+    first = torch.ones(6, Hk, D)
+    append_ref(kp, vp, blocks, 0, first, first)
+    patch = torch.full((2, Hk, D), 5.0)
+    append_ref(kp, vp, blocks, 3, patch, -patch)
+    got = gather_ref(kp, blocks, 6)
+    assert torch.equal(got[:3], first[:3]) and torch.equal(got[3:5], patch) and torch.equal(got[5:], first[5:])
+    assert torch.equal(gather_ref(vp, blocks, 6)[3:5], -patch)
