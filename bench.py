@@ -18,8 +18,11 @@ The same line carries
                 timed while rotating over >= 512 MiB of KV pool copies so the
                 256 MiB Infinity Cache cannot hold them; the paged KV append
                 of a prefill (4 x 2048 tokens) and of a decode step (32 x 1
-                token) in GB/s of bytes read + written; and the S=16384
-                D=128 bf16 prefill in TFLOP/s.
+                token) in GB/s of bytes read + written; one layer's
+                attention section of a decode step (batched append + paged
+                attention) beside the reference's per-sequence
+                append / gather / dense structure; and the S=16384 D=128
+                bf16 prefill in TFLOP/s.
 """
 
 from __future__ import annotations
@@ -201,6 +204,49 @@ class AppendLaunch:
             _lib.check(rc)
 
 
+def decode_step_times(dev, iters=20):
+    """One layer's attention section for a decode step of the decode_b32 shape
+    (32 sequences, contexts 256..4096, 32/8 heads, D=64, fp16): the batched
+    paged path (append_batch + paged attention, one launch each) against the
+    reference's per-sequence structure (append, gather of the whole history,
+    dense causal attention; engine/model/block.py:57-71), both on the GPU."""
+    import torch
+
+    from engine.attention import flash_attention
+    from engine.cache import KVCacheConfig, PagedKVCache
+    from engine.model import attention_section
+
+    g = torch.Generator().manual_seed(2)
+    ctx = torch.randint(256, 4097, (32,), generator=g).tolist()
+    nb = sum(-(-(c + 1) // 16) for c in ctx) + 64
+    cache = PagedKVCache(KVCacheConfig(1, 8, 64, nb, 16, torch.float16, dev))
+    tables = [cache.new_sequence() for _ in ctx]
+    for t, c in zip(tables, ctx):
+        cache.prepare_step([t], c - 1)  # history of c - 1 tokens (pool contents are irrelevant to timing)
+    starts = [t.length for t in tables]
+    step = cache.prepare_step(tables, 1, starts)  # the new token of this step
+    q = torch.randn(32, 32, 1, 64, generator=g).half().to(dev)
+    k = torch.randn(32, 8, 1, 64, generator=g).half().to(dev)
+    v = torch.randn(32, 8, 1, 64, generator=g).half().to(dev)
+
+    def paged(i=0):
+        attention_section(q, k, v, 0, cache, tables, starts, step)
+
+    def per_sequence(i=0):
+        for b, t in enumerate(tables):
+            cache.append(0, t, k[b].transpose(0, 1), v[b].transpose(0, 1), start=starts[b])
+            kd, vd = cache.gather(0, t)
+            flash_attention(q[b:b + 1], kd.transpose(0, 1).unsqueeze(0), vd.transpose(0, 1).unsqueeze(0),
+                            causal=True, scale=0.125)
+
+    t_paged = event_time_ms(paged, iters, 3)
+    t_ref = event_time_ms(per_sequence, max(3, iters // 4), 1)
+    del cache
+    torch.cuda.empty_cache()
+    return {"us": round(t_paged * 1e3, 2), "per_sequence_gather_path_us": round(t_ref * 1e3, 1),
+            "speedup": round(t_ref / t_paged, 1)}
+
+
 def event_time_ms(fn, n, warmup, trials=3):
     """Median over trials of (HIP-event time of n back-to-back launches) / n."""
     import torch
@@ -299,6 +345,7 @@ def main():
             extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
                            "bytes": int(al.bytes), "copies": al.copies, "dtype": "fp16"}
             del al
+        extra["decode_step_b32_one_layer"] = decode_step_times(dev)
         c5 = workloads.prefill_s16384()
         f5 = FlashLaunch(c5, dev)
         ms = event_time_ms(f5, 5, 1)

@@ -206,6 +206,20 @@ class PagedKVCache:
                 done += n
         table.length = max(table.length, end)
 
+    def prepare_step(self, tables: Sequence[BlockTable], num_new: int, starts: Sequence[int] | None = None
+                     ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Host side of one engine step for a batch: allocate the blocks the
+        ``num_new`` tokens of every sequence need (at ``starts[b]``, default
+        each table's end), extend the lengths, and return the int32 device
+        block table + context lengths that every layer's ``append_batch`` and
+        ``paged_attention`` of the step share (one host-to-device copy)."""
+        starts = [t.length for t in tables] if starts is None else list(starts)
+        for t, s0 in zip(tables, starts):
+            while len(t.blocks) < t.num_blocks_needed(s0 + num_new):
+                t.blocks.append(self._alloc_block())
+            t.length = max(t.length, s0 + num_new)
+        return block_table_tensor(tables, self.device)
+
     def append_batch(self, layer: int, tables: Sequence[BlockTable], k: torch.Tensor, v: torch.Tensor,
                      lengths: Sequence[int], starts: Sequence[int] | None = None,
                      block_tables: torch.Tensor | None = None) -> None:

@@ -160,3 +160,47 @@ def test_append_batch_then_paged_attention_equals_gather_path():
         assert (out[b:b + 1].float() - ref.float()).abs().max().item() <= 2e-3
         row = sum(lens[:b])
         assert torch.equal(kd, k[row:row + lens[b]]) and torch.equal(vd, v[row:row + lens[b]])
+
+
+@pytest.mark.parametrize("L,dtype", [(1, torch.float16), (5, torch.bfloat16)])
+def test_attention_section_matches_reference_per_sequence_path(L, dtype):
+    """engine.model.attention_section (batched, paged) against the reference's
+    per-sequence sequence of block.py:56-75 on the oracle: append_ref, then
+    gather_ref of the whole history, then flash_attention_ref with causal=True
+    and scale 1/sqrt(D), transposed to (L, Hq * D)."""
+    import math
+
+    from engine.model import attention_section
+    from oracle import flash_attention_ref, gather_ref
+
+    B, Hq, Hk, D, bs = 4, 8, 2, 64, 16
+    cfg = KVCacheConfig(num_layers=2, num_kv_heads=Hk, head_dim=D, num_blocks=80, block_size=bs,
+                        dtype=dtype, device=DEV)
+    cache = PagedKVCache(cfg)
+    g = torch.Generator().manual_seed(40 + L)
+    tables = [cache.new_sequence() for _ in range(B)]
+    hist = [37, 0, 100, 16]
+    # existing history (layer 1), written through the cache's own append
+    for t, n in zip(tables, hist):
+        if n:
+            cache.append(1, t, torch.randn(n, Hk, D, generator=g).to(dtype).to(DEV),
+                         torch.randn(n, Hk, D, generator=g).to(dtype).to(DEV))
+    ref_k = cache.k[1].cpu().float()
+    ref_v = cache.v[1].cpu().float()
+    starts = [t.length for t in tables]
+    q = torch.randn(B, Hq, L, D, generator=g).to(dtype)
+    k = torch.randn(B, Hk, L, D, generator=g).to(dtype)
+    v = torch.randn(B, Hk, L, D, generator=g).to(dtype)
+    step = cache.prepare_step(tables, L, starts)
+    out = attention_section(q.to(DEV), k.to(DEV), v.to(DEV), 1, cache, tables, starts, step)
+    assert out.shape == (B, L, Hq * D)
+    tol = 2e-3 if dtype == torch.float16 else 1e-2
+    for b, t in enumerate(tables):
+        append_ref(ref_k, ref_v, t.blocks, starts[b], k[b].transpose(0, 1).float(), v[b].transpose(0, 1).float())
+        kd = gather_ref(ref_k, t.blocks, t.length).transpose(0, 1).unsqueeze(0)
+        vd = gather_ref(ref_v, t.blocks, t.length).transpose(0, 1).unsqueeze(0)
+        ref = flash_attention_ref(q[b:b + 1].float(), kd, vd, causal=True, scale=1.0 / math.sqrt(D))
+        ref = ref.transpose(1, 2).reshape(1, L, Hq * D)
+        err = (out[b:b + 1].float().cpu() - ref).abs().max().item()
+        assert err <= tol, (b, err)
+    assert torch.equal(cache.k[1].cpu().float(), ref_k) and torch.equal(cache.v[1].cpu().float(), ref_v)
