@@ -18,11 +18,14 @@ The same line carries
                 timed while rotating over >= 512 MiB of KV pool copies so the
                 256 MiB Infinity Cache cannot hold them; the paged KV append
                 of a prefill (4 x 2048 tokens) and of a decode step (32 x 1
-                token) in GB/s of bytes read + written; one layer's
-                attention section of a decode step (batched append + paged
-                attention) beside the reference's per-sequence
-                append / gather / dense structure; and the S=16384 D=128
-                bf16 prefill in TFLOP/s.
+                token) in GB/s of bytes read + written; RoPE of the
+                prefill's q (4 x 32 x 2048 x 64) in GB/s; one layer's
+                attention section of that prefill with RoPE fused against
+                rope_apply first; one layer's attention section of a decode
+                step (batched append + paged attention; eager, HIP-graph
+                replay, with RoPE fused or applied first) beside the
+                reference's per-sequence append / gather / dense
+                structure; and the S=16384 D=128 bf16 prefill in TFLOP/s.
 """
 
 from __future__ import annotations
@@ -204,6 +207,98 @@ class AppendLaunch:
             _lib.check(rc)
 
 
+class RopeLaunch:
+    """Pre-bound cie_rope_apply, in place, on q of the prefill_s2048 shape
+    (4 x 32 heads x 2048 rows x 64, fp16) at positions 0..2047, rotating over
+    copies that together exceed `min_bytes` (Infinity Cache)."""
+
+    def __init__(self, dev, B=4, H=32, L=2048, D=64, min_bytes=512 << 20):
+        import torch
+        from engine import _lib
+        from engine.model.rope import build_rope_cache
+
+        self.lib = _lib.load()
+        cos, sin = build_rope_cache(4096, D)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        per = B * H * L * D * 2
+        self.copies = max(1, -(-min_bytes // per))
+        x = torch.randn(B, H, L, D).half().to(dev)
+        self.bufs = [x.clone() for _ in range(self.copies)]
+        self._st = _lib.strides(x)
+        self.tail = (self._st, self._st, None, 0, self.cos.data_ptr(), self.sin.data_ptr(), 4096, None,
+                     B, H, L, D, 0, _lib.stream_handle(dev))
+        self.bytes = 2 * per  # read once, written once (the fp32 tables: 0.5 MiB more, from L2)
+
+    def __call__(self, i=0):
+        t = self.bufs[i % self.copies]
+        rc = self.lib.cie_rope_apply(t.data_ptr(), t.data_ptr(), *self.tail)
+        if rc:
+            from engine import _lib
+            _lib.check(rc)
+
+
+def prefill_section_times(dev, iters=10):
+    """One layer's attention section for a prefill of 4 fresh sequences x
+    2048 tokens (32/8 heads, D=64, fp16) with RoPE: fused (rotary append that
+    also returns the rotated K, Q rotated in the prefill kernel's load)
+    against rotating q and k first with rope_apply and running the plain
+    section (append + prefill attention)."""
+    import torch
+
+    from engine.cache import KVCacheConfig, PagedKVCache
+    from engine.model import attention_section
+    from engine.model.rope import RotaryEmbedding, rope_apply
+
+    B, L, Hq, Hk, D = 4, 2048, 32, 8, 64
+    emb = RotaryEmbedding(D, 4096).to(dev)
+    cache = PagedKVCache(KVCacheConfig(1, Hk, D, B * L // 16 + 8, 16, torch.float16, dev))
+    tables = [cache.new_sequence() for _ in range(B)]
+    step = cache.prepare_step(tables, L)
+    g = torch.Generator().manual_seed(8)
+    # transposed views of (B, L, H, D) projections, as the model makes them (block.py:50-52)
+    q = (torch.randn(B, L, Hq, D, generator=g) / 8).half().to(dev).transpose(1, 2)
+    k = torch.randn(B, L, Hk, D, generator=g).half().to(dev).transpose(1, 2)
+    v = torch.randn(B, L, Hk, D, generator=g).half().to(dev).transpose(1, 2)
+
+    def fused(i=0):
+        attention_section(q, k, v, 0, cache, step, rope=emb.tables)
+
+    def unfused(i=0):
+        qr = rope_apply(q, emb.cos, emb.sin)
+        kr = rope_apply(k, emb.cos, emb.sin)
+        attention_section(qr, kr, v, 0, cache, step)
+
+    def plain(i=0):
+        attention_section(q, k, v, 0, cache, step)
+
+    # GPU time of each section: captured in a HIP graph and replayed
+    res = {}
+    for name, fn in (("fused_us", fused), ("rope_apply_then_section_us", unfused), ("no_rope_us", plain)):
+        gr = _captured(fn)
+        res[name] = round(event_time_ms(lambda i=0: gr.replay(), iters, 2) * 1e3, 1)
+        del gr
+    del cache
+    torch.cuda.empty_cache()
+    res["rope_cost_fused_us"] = round(res["fused_us"] - res["no_rope_us"], 1)
+    res["rope_cost_unfused_us"] = round(res["rope_apply_then_section_us"] - res["no_rope_us"], 1)
+    return res
+
+
+def _captured(fn):
+    """fn captured once in a HIP graph (after one eager warm-up on a side stream)."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
 def decode_step_times(dev, iters=20):
     """One layer's attention section for a decode step of the decode_b32 shape
     (32 sequences, contexts 256..4096, 32/8 heads, D=64, fp16): the batched
@@ -223,14 +318,33 @@ def decode_step_times(dev, iters=20):
     tables = [cache.new_sequence() for _ in ctx]
     for t, c in zip(tables, ctx):
         cache.prepare_step([t], c - 1)  # history of c - 1 tokens (pool contents are irrelevant to timing)
-    starts = [t.length for t in tables]
-    step = cache.prepare_step(tables, 1, starts)  # the new token of this step
-    q = torch.randn(32, 32, 1, 64, generator=g).half().to(dev)
-    k = torch.randn(32, 8, 1, 64, generator=g).half().to(dev)
-    v = torch.randn(32, 8, 1, 64, generator=g).half().to(dev)
+    step = cache.prepare_step(tables, 1)  # the new token of this step
+    starts = [t.length - 1 for t in tables]
+    # transposed views of (B, L, H, D) projections, as the model makes them (block.py:50-52)
+    q = torch.randn(32, 1, 32, 64, generator=g).half().to(dev).transpose(1, 2)
+    k = torch.randn(32, 1, 8, 64, generator=g).half().to(dev).transpose(1, 2)
+    v = torch.randn(32, 1, 8, 64, generator=g).half().to(dev).transpose(1, 2)
+
+    from engine.model.rope import RotaryEmbedding, rope_apply
+
+    emb = RotaryEmbedding(64, 8192).to(dev)
 
     def paged(i=0):
-        attention_section(q, k, v, 0, cache, tables, starts, step)
+        attention_section(q, k, v, 0, cache, step)
+
+    def paged_rope(i=0):
+        attention_section(q, k, v, 0, cache, step, rope=emb.tables)
+
+    def paged_rope_unfused(i=0):
+        pos = step.context_lens[:, None] - 1
+        attention_section(rope_apply(q, emb.cos, emb.sin, pos), rope_apply(k, emb.cos, emb.sin, pos), v, 0, cache,
+                          step)
+
+
+    # the same section captured once in a HIP graph and replayed (no host work per layer)
+    graph = _captured(paged)
+    graph_rope = _captured(paged_rope)
+    graph_rope_unfused = _captured(paged_rope_unfused)
 
     def per_sequence(i=0):
         for b, t in enumerate(tables):
@@ -240,19 +354,45 @@ def decode_step_times(dev, iters=20):
                             causal=True, scale=0.125)
 
     t_paged = event_time_ms(paged, iters, 3)
+    t_graph = event_time_ms(lambda i=0: graph.replay(), iters, 3)
+    t_graph_rope = event_time_ms(lambda i=0: graph_rope.replay(), iters, 3)
+    t_graph_rope_unfused = event_time_ms(lambda i=0: graph_rope_unfused.replay(), iters, 3)
     t_ref = event_time_ms(per_sequence, max(3, iters // 4), 1)
-    del cache
+    del graph, graph_rope, graph_rope_unfused, cache
     torch.cuda.empty_cache()
-    return {"us": round(t_paged * 1e3, 2), "per_sequence_gather_path_us": round(t_ref * 1e3, 1),
-            "speedup": round(t_ref / t_paged, 1)}
+    return {"us": round(t_paged * 1e3, 2), "graph_replay_us": round(t_graph * 1e3, 2),
+            "graph_replay_rope_fused_us": round(t_graph_rope * 1e3, 2),
+            "graph_replay_rope_apply_then_section_us": round(t_graph_rope_unfused * 1e3, 2),
+            "per_sequence_gather_path_us": round(t_ref * 1e3, 1), "speedup": round(t_ref / t_paged, 1)}
+
+
+SETTLE_S = 0.3  # seconds of untimed back-to-back work before a measurement
+
+
+def settle(fn, seconds=SETTLE_S):
+    """Run fn back-to-back, untimed, for about `seconds`: the GPU needs a few
+    milliseconds of sustained load before its clock reaches the level it
+    holds under continuous work (the first 40 prefill launches after idle
+    run 10-15 % slower than the following ones)."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
 
 
 def event_time_ms(fn, n, warmup, trials=3):
-    """Median over trials of (HIP-event time of n back-to-back launches) / n."""
+    """Median over trials of (HIP-event time of n back-to-back launches) / n,
+    after `warmup` launches and a settle phase."""
     import torch
 
     for i in range(warmup):
         fn(i)
+    settle(fn)
     torch.cuda.synchronize()
     res = []
     for _ in range(trials):
@@ -307,7 +447,8 @@ def main():
     case = workloads.prefill_s2048()
     q, k, v = case.q.to(dev), case.k.to(dev), case.v.to(dev)
 
-    # headline: K steps of the public entry point
+    # headline: K steps of the public entry point (after an untimed clock settle and W warmup steps)
+    settle(lambda i=0: flash_attention(q, k, v, causal=True))
     for _ in range(args.warmup):
         flash_attention(q, k, v, causal=True)
     torch.cuda.synchronize()
@@ -345,6 +486,14 @@ def main():
             extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
                            "bytes": int(al.bytes), "copies": al.copies, "dtype": "fp16"}
             del al
+        rl = RopeLaunch(dev)
+        ms = event_time_ms(rl, max(50, 4 * rl.copies), rl.copies)
+        gbs = rl.bytes / (ms / 1e3) / 1e9
+        extra["rope_q_prefill_b4_s2048"] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                            "us": round(ms * 1e3, 2), "bytes": int(rl.bytes), "copies": rl.copies,
+                                            "dtype": "fp16"}
+        del rl
+        extra["prefill_section_b4_s2048_rope"] = prefill_section_times(dev)
         extra["decode_step_b32_one_layer"] = decode_step_times(dev)
         c5 = workloads.prefill_s16384()
         f5 = FlashLaunch(c5, dev)

@@ -73,6 +73,14 @@ void set_scale(float scale, float* c, uint32_t* q_sign) {
   *c = std::max(std::fabs(scale) * cie::kLog2e, 1e-30f);
 }
 
+// cos / sin: fp32 (rows, D/2) row-major tables, as RotaryEmbedding holds them.
+int check_rope(const float* cos, const float* sin, int rows) {
+  if (!cos || !sin) return fail(CIE_EINVAL, "rope tables: NULL pointer");
+  if (!aligned16(cos) || !aligned16(sin)) return fail(CIE_EINVAL, "rope tables: pointer is not 16-byte aligned");
+  if (rows < 1) return fail(CIE_EINVAL, "rope tables need at least one row, got %d", rows);
+  return CIE_OK;
+}
+
 #define CIE_TRY(x)             \
   do {                         \
     int _rc = (x);             \
@@ -87,11 +95,14 @@ int cie_abi_version(void) { return CIE_ABI_VERSION; }
 
 const char* cie_last_error(void) { return g_err.c_str(); }
 
-int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
-                  const int64_t* q_stride, const int64_t* k_stride,
-                  const int64_t* v_stride, const int64_t* o_stride,
-                  int B, int Hq, int Hk, int Lq, int Lk, int D,
-                  float scale, int causal, int dtype, void* stream) {
+}  // extern "C"
+
+static int flash_impl(const void* q, const void* k, const void* v, void* o,
+                      const int64_t* q_stride, const int64_t* k_stride,
+                      const int64_t* v_stride, const int64_t* o_stride,
+                      int B, int Hq, int Hk, int Lq, int Lk, int D,
+                      float scale, int causal, int dtype, void* stream,
+                      cie::RopeTables rope, const int32_t* q_pos0) {
   CIE_TRY(common_checks(Hq, Hk, D, dtype));
   if (B < 0 || Lq < 0 || Lk < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d, Lk=%d)", B, Lq, Lk);
   if (!std::isfinite(scale)) return fail(CIE_EINVAL, "scale must be finite");
@@ -129,7 +140,32 @@ int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
   p.n_wg = (int)n_wg;
   set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
+  p.rope = rope;
+  p.q_pos0 = q_pos0;
   return launch_status(cie::launch_flash(p, dtype, D, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" {
+
+int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
+                  const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride,
+                  int B, int Hq, int Hk, int Lq, int Lk, int D,
+                  float scale, int causal, int dtype, void* stream) {
+  return flash_impl(q, k, v, o, q_stride, k_stride, v_stride, o_stride, B, Hq, Hk, Lq, Lk, D, scale, causal,
+                    dtype, stream, cie::RopeTables{nullptr, nullptr, 0}, nullptr);
+}
+
+int cie_flash_fwd_rope(const void* q, const void* k, const void* v, void* o,
+                       const int64_t* q_stride, const int64_t* k_stride,
+                       const int64_t* v_stride, const int64_t* o_stride,
+                       int B, int Hq, int Hk, int Lq, int Lk, int D,
+                       float scale, int causal, int dtype,
+                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const int32_t* q_pos0, void* stream) {
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  return flash_impl(q, k, v, o, q_stride, k_stride, v_stride, o_stride, B, Hq, Hk, Lq, Lk, D, scale, causal,
+                    dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, q_pos0);
 }
 
 // Largest valid context length: the table bound, tightened by the caller's hint.
@@ -149,15 +185,17 @@ size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D, int max_c
   return g.ok ? g.info_bytes + g.slot_bytes : 0;
 }
 
-int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
-                  const int32_t* block_tables, const int32_t* context_lens,
-                  void* o, void* workspace, size_t workspace_bytes,
-                  const int64_t* q_stride, const int64_t* kc_stride,
-                  const int64_t* vc_stride, const int64_t* o_stride,
-                  int B, int Hq, int Hk, int Lq, int D,
-                  int num_blocks, int block_size, int max_blocks_per_seq,
-                  int max_context, float scale, int causal, int dtype,
-                  void* stream) {
+}  // extern "C"
+
+static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* block_tables, const int32_t* context_lens,
+                      void* o, void* workspace, size_t workspace_bytes,
+                      const int64_t* q_stride, const int64_t* kc_stride,
+                      const int64_t* vc_stride, const int64_t* o_stride,
+                      int B, int Hq, int Hk, int Lq, int D,
+                      int num_blocks, int block_size, int max_blocks_per_seq,
+                      int max_context, float scale, int causal, int dtype,
+                      void* stream, cie::RopeTables rope) {
   CIE_TRY(common_checks(Hq, Hk, D, dtype));
   if (B < 0 || Lq < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d)", B, Lq);
   if (block_size < 1) return fail(CIE_EINVAL, "block_size must be positive, got %d", block_size);
@@ -228,15 +266,51 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   p.Hg = g.Hg; p.NG = g.NG; p.n_qt = g.n_qt; p.NWV = g.NWV; p.NCH = g.NCH; p.NST = g.NST; p.Wg = g.Wg;
   set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
+  p.rope = rope;
   return launch_status(cie::launch_paged(p, dtype, D, g.lds_bytes, static_cast<hipStream_t>(stream)));
 }
 
-int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
-                  const int64_t* new_stride, const int64_t* v_new_stride,
-                  const int64_t* kc_stride, const int64_t* vc_stride,
-                  const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
-                  uint32_t* status, int B, int T, int max_new, int Hk, int D,
-                  int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream) {
+extern "C" {
+
+int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
+                  const int32_t* block_tables, const int32_t* context_lens,
+                  void* o, void* workspace, size_t workspace_bytes,
+                  const int64_t* q_stride, const int64_t* kc_stride,
+                  const int64_t* vc_stride, const int64_t* o_stride,
+                  int B, int Hq, int Hk, int Lq, int D,
+                  int num_blocks, int block_size, int max_blocks_per_seq,
+                  int max_context, float scale, int causal, int dtype,
+                  void* stream) {
+  return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
+                    kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
+                    max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0});
+}
+
+int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* block_tables, const int32_t* context_lens,
+                       void* o, void* workspace, size_t workspace_bytes,
+                       const int64_t* q_stride, const int64_t* kc_stride,
+                       const int64_t* vc_stride, const int64_t* o_stride,
+                       int B, int Hq, int Hk, int Lq, int D,
+                       int num_blocks, int block_size, int max_blocks_per_seq,
+                       int max_context, float scale, int causal, int dtype,
+                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       void* stream) {
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
+                    kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
+                    max_context, scale, causal, dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows});
+}
+
+}  // extern "C"
+
+static int append_impl(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const int64_t* new_stride, const int64_t* v_new_stride,
+                       const int64_t* kc_stride, const int64_t* vc_stride,
+                       const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
+                       uint32_t* status, int B, int T, int max_new, int Hk, int D,
+                       int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream,
+                       cie::RopeTables rope, void* k_out, const int64_t* k_out_stride) {
   if (dtype != CIE_DTYPE_F16 && dtype != CIE_DTYPE_BF16)
     return fail(CIE_EDTYPE, "unsupported dtype code %d (f16 = 0, bf16 = 1)", dtype);
   if (!head_dim_ok(D)) return fail(CIE_EHEADDIM, "head_dim must be a power of 2 in [16, 256], got %d", D);
@@ -288,7 +362,83 @@ int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
   p.lg_cph = (uint32_t)__builtin_ctz((unsigned)(D / 8));
   p.cprdiv = cie::make_fastdiv(p.cpr);
   p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
-  return launch_status(cie::launch_kv_append(p, B, max_new, static_cast<hipStream_t>(stream)));
+  p.rope = rope;
+  p.updiv = cie::make_fastdiv(p.cpr / 2);
+  if (k_out) {
+    if (!rope.cos) return fail(CIE_EINVAL, "k_out is only written by the rotary append");
+    CIE_TRY(check_ptr("k_out", k_out));
+    if (!k_out_stride) return fail(CIE_EINVAL, "k_out: stride array is NULL");
+    const int64_t os[4] = {0, k_out_stride[0], k_out_stride[1], k_out_stride[2]};
+    CIE_TRY(check_strides("k_out", os));
+    p.k_out = static_cast<uint16_t*>(k_out);
+    p.os0 = os[1];
+    p.os1 = os[2];
+  }
+  return launch_status(cie::launch_kv_append(p, B, max_new, dtype, D, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" {
+
+int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                  const int64_t* new_stride, const int64_t* v_new_stride,
+                  const int64_t* kc_stride, const int64_t* vc_stride,
+                  const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
+                  uint32_t* status, int B, int T, int max_new, int Hk, int D,
+                  int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream) {
+  return append_impl(k_new, v_new, k_cache, v_cache, new_stride, v_new_stride, kc_stride, vc_stride, block_tables,
+                     cu_new, start, status, B, T, max_new, Hk, D, num_blocks, block_size, max_blocks_per_seq, dtype,
+                     stream, cie::RopeTables{nullptr, nullptr, 0}, nullptr, nullptr);
+}
+
+int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const int64_t* new_stride, const int64_t* v_new_stride,
+                       const int64_t* kc_stride, const int64_t* vc_stride,
+                       const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
+                       uint32_t* status, int B, int T, int max_new, int Hk, int D,
+                       int num_blocks, int block_size, int max_blocks_per_seq, int dtype,
+                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       void* k_out, const int64_t* k_out_stride, void* stream) {
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  return append_impl(k_new, v_new, k_cache, v_cache, new_stride, v_new_stride, kc_stride, vc_stride, block_tables,
+                     cu_new, start, status, B, T, max_new, Hk, D, num_blocks, block_size, max_blocks_per_seq, dtype,
+                     stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, k_out, k_out_stride);
+}
+
+int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int64_t* out_stride,
+                   const int32_t* positions, int64_t pos_batch_stride,
+                   const float* rope_cos, const float* rope_sin, int rope_rows,
+                   uint32_t* status, int B, int H, int L, int D, int dtype, void* stream) {
+  if (dtype != CIE_DTYPE_F16 && dtype != CIE_DTYPE_BF16)
+    return fail(CIE_EDTYPE, "unsupported dtype code %d (f16 = 0, bf16 = 1)", dtype);
+  if (!head_dim_ok(D)) return fail(CIE_EHEADDIM, "head_dim must be a power of 2 in [16, 256], got %d", D);
+  if (B < 0 || H < 0 || L < 0 || pos_batch_stride < 0)
+    return fail(CIE_EINVAL, "invalid sizes (B=%d, H=%d, L=%d, pos_batch_stride=%lld)", B, H, L,
+                (long long)pos_batch_stride);
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  const int64_t total = (int64_t)B * H * L * (D / 16);
+  if (total >= ((int64_t)1 << 31)) return fail(CIE_EINVAL, "too many rows for one launch");
+  if (total == 0) {
+    g_err.clear();
+    return CIE_OK;
+  }
+  CIE_TRY(check_ptr("x", x));
+  CIE_TRY(check_ptr("out", out));
+  CIE_TRY(check_strides("x", x_stride));
+  CIE_TRY(check_strides("out", out_stride));
+  cie::RopeParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.out = static_cast<uint16_t*>(out);
+  p.xs0 = x_stride[0]; p.xs1 = x_stride[1]; p.xs2 = x_stride[2];
+  p.os0 = out_stride[0]; p.os1 = out_stride[1]; p.os2 = out_stride[2];
+  p.pos = positions;
+  p.pos_bs = pos_batch_stride;
+  p.tab = cie::RopeTables{rope_cos, rope_sin, rope_rows};
+  p.status = status;
+  p.B = B; p.H = H; p.L = L;
+  p.total = (uint32_t)total;
+  p.ldiv = cie::make_fastdiv((uint32_t)L);
+  p.hdiv = cie::make_fastdiv((uint32_t)H);
+  return launch_status(cie::launch_rope(p, dtype, D, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

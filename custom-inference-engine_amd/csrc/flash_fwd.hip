@@ -29,6 +29,7 @@
 // when no row needs it. The final acc / l is unchanged by the choice of m.
 // l accumulates the probabilities as rounded for the P.V product.
 #include "kernels.hpp"
+#include "rope.hpp"
 
 namespace cie {
 
@@ -93,10 +94,12 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   const uint16_t* qrow = p.q + b * p.qs0 + hq * p.qs1 + (int64_t)qi * p.qs2;
   u32x4 qf[C::KK];
 #pragma unroll
-  for (int kk = 0; kk < C::KK; ++kk) {
-    qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
-    qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
-  }
+  for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
+  if (p.rope.cos)  // RoPE fused into the load: row qi at position q_pos0[b] + qi
+    rope_q_lane<DTYPE, D>(qf, p.rope.cos, p.rope.sin, p.rope.rows, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq,
+                          hl);
+#pragma unroll
+  for (int kk = 0; kk < C::KK; ++kk) qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
 
   // Key range of the workgroup and of this wave; lim = last key this row sees.
   const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;

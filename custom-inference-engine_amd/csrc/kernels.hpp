@@ -10,6 +10,14 @@
 
 namespace cie {
 
+// Rotary tables of the kernels that apply RoPE: cos, sin fp32 (rows, D/2),
+// contiguous. cos == nullptr: no rotation.
+struct RopeTables {
+  const float* cos;
+  const float* sin;
+  int rows;
+};
+
 // Dense attention. Strides are in elements; head_dim stride is 1.
 struct FlashParams {
   const uint16_t* q;
@@ -26,6 +34,8 @@ struct FlashParams {
   float scale_log2;  // |scale| * log2(e), never below 1e-30
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
   int causal;
+  RopeTables rope;        // rotate q rows as they are loaded: row i of batch b at position q_pos0[b] + i
+  const int32_t* q_pos0;  // [B] or nullptr (position = row)
 };
 
 // Paged attention over a (num_blocks, block_size, Hk, D) pool.
@@ -58,6 +68,7 @@ struct PagedParams {
   float scale_log2;  // |scale| * log2(e), never below 1e-30
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
   int causal;
+  RopeTables rope;  // rotate q row i of sequence b at position lens[b] - Lq + i as it is loaded
 };
 
 constexpr int kPagedTile = 32;         // tokens per tile
@@ -100,10 +111,33 @@ struct AppendParams {
   uint32_t cpr;           // 16-byte chunks per token row (Hk * D / 8)
   uint32_t lg_cph;        // log2 of chunks per head row (D / 8)
   FastDiv cprdiv, bsdiv;
+  // RoPE on K (rope.cos != nullptr): token i of sequence b is rotated at
+  // position start[b] + i before it is written; a position outside the
+  // table writes neither K nor V of that token and ORs 2 into status.
+  RopeTables rope;
+  FastDiv updiv;          // chunk pairs per token row (cpr / 2)
+  uint16_t* k_out;        // optional dense copy of the rotated K rows, (T, Hk, D)
+  int64_t os0, os1;       // k_out strides (token, head)
+};
+
+// Standalone RoPE of x (B, H, L, D) into out (may be x itself).
+struct RopeParams {
+  const uint16_t* x;
+  uint16_t* out;
+  int64_t xs0, xs1, xs2;
+  int64_t os0, os1, os2;
+  const int32_t* pos;  // nullptr: position = row index l; else pos[b * pos_bs + l]
+  int64_t pos_bs;
+  RopeTables tab;
+  uint32_t* status;    // optional: 2 ORed in when a position is outside the table
+  int B, H, L;
+  uint32_t total;      // B * H * L * D / 16 chunk pairs
+  FastDiv ldiv, hdiv;
 };
 
 hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stream);
-hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, hipStream_t stream);
+hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, int dtype, int D, hipStream_t stream);
+hipError_t launch_rope(const RopeParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, hipStream_t stream);
 
 }  // namespace cie

@@ -17,6 +17,7 @@
 // [0, num_blocks) is never written; the launch then sets *status to 1 when a
 // status word is given.
 #include "kernels.hpp"
+#include "rope.hpp"
 
 namespace cie {
 
@@ -70,8 +71,100 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
   if (p.status && __builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(p.status, 1u);
 }
 
-hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, hipStream_t stream) {
+// With RoPE on K (rope/rope.hpp restates kernels/ref/rope_apply_ref.py:46-53):
+// one thread moves the chunk pair (j, j + D/16) of one head of one token, K
+// rotated at position start[b] + i through the fp32 tables, V copied, both
+// pairs written to the pool and the rotated K optionally also to the dense
+// k_out rows (what prefill attention over the new tokens reads).
+constexpr int kRopeUnroll = 2;
+
+template <int DTYPE>
+__global__ __launch_bounds__(256) void kv_append_rope_kernel(const AppendParams p) {
+  const int b = blockIdx.y;
+  const int n0 = p.cu_new[b];
+  const int L = p.cu_new[b + 1] - n0;
+  if (L <= 0) return;
+  const int start = p.start[b];
+  const uint32_t upr = p.cpr >> 1;            // chunk pairs per token row
+  const uint32_t total = (uint32_t)L * upr;
+  const uint32_t lg_half = p.lg_cph - 1u;     // log2(D / 16)
+  const int half = 4 << p.lg_cph;             // D / 2 elements
+  const int32_t* btr = p.bt + (int64_t)b * p.max_blocks;
+  const int limit = p.max_blocks * p.block_size;
+  const uint32_t stride = gridDim.x * 256u;
+  uint32_t bad = 0;
+  for (uint32_t c0 = blockIdx.x * 256u + threadIdx.x; c0 < total; c0 += kRopeUnroll * stride) {
+    u32x4 klo[kRopeUnroll], khi[kRopeUnroll], vlo[kRopeUnroll], vhi[kRopeUnroll];
+    f32x8 cs[kRopeUnroll], sn[kRopeUnroll];
+    int64_t dk[kRopeUnroll], dv[kRopeUnroll], dout[kRopeUnroll];
+    bool in[kRopeUnroll], ok[kRopeUnroll];
+#pragma unroll
+    for (int u = 0; u < kRopeUnroll; ++u) {
+      const uint32_t c = c0 + u * stride;
+      in[u] = c < total;
+      const uint32_t cc = in[u] ? c : c0;  // clamped: every load stays inside the sources
+      const uint32_t i = fdiv(cc, p.updiv);
+      const uint32_t ch = cc - i * upr;
+      const uint32_t h = ch >> lg_half, j = ch & ((1u << lg_half) - 1u);
+      const int pos = start + (int)i;
+      const bool rope_ok = pos >= 0 && pos < p.rope.rows;
+      const bool pos_ok = pos >= 0 && pos < limit;
+      const int blk = pos_ok ? (int)fdiv((uint32_t)pos, p.bsdiv) : 0;
+      const int off = pos_ok ? pos - blk * p.block_size : 0;
+      const int bid = pos_ok ? btr[blk] : -1;
+      const bool bid_ok = (uint32_t)bid < (uint32_t)p.num_blocks;
+      ok[u] = in[u] && rope_ok && pos_ok && bid_ok;
+      bad |= (in[u] && !(pos_ok && bid_ok)) ? 1u : 0u;
+      bad |= (in[u] && !rope_ok) ? 2u : 0u;
+      in[u] = in[u] && rope_ok;
+      const int64_t row = (int64_t)(n0 + (int)i);
+      const uint16_t* ks = p.k_new + row * p.ns0 + h * p.ns1 + 8 * j;
+      const uint16_t* vs = p.v_new + row * p.ms0 + h * p.ms1 + 8 * j;
+      klo[u] = *reinterpret_cast<const u32x4*>(ks);
+      khi[u] = *reinterpret_cast<const u32x4*>(ks + half);
+      vlo[u] = *reinterpret_cast<const u32x4*>(vs);
+      vhi[u] = *reinterpret_cast<const u32x4*>(vs + half);
+      const int64_t tr = (rope_ok ? (int64_t)pos : 0) * half + 8 * j;
+      cs[u] = tab8(p.rope.cos + tr);
+      sn[u] = tab8(p.rope.sin + tr);
+      dk[u] = (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 + h * p.ks2 + 8 * j;
+      dv[u] = (int64_t)bid * p.vs0 + (int64_t)off * p.vs1 + h * p.vs2 + 8 * j;
+      dout[u] = row * p.os0 + h * p.os1 + 8 * j;
+    }
+#pragma unroll
+    for (int u = 0; u < kRopeUnroll; ++u) {
+      rope8<DTYPE>(klo[u], khi[u], cs[u], sn[u]);
+      if (ok[u]) {
+        *reinterpret_cast<u32x4*>(p.kc + dk[u]) = klo[u];
+        *reinterpret_cast<u32x4*>(p.kc + dk[u] + half) = khi[u];
+        *reinterpret_cast<u32x4*>(p.vc + dv[u]) = vlo[u];
+        *reinterpret_cast<u32x4*>(p.vc + dv[u] + half) = vhi[u];
+      }
+      if (p.k_out && in[u]) {
+        *reinterpret_cast<u32x4*>(p.k_out + dout[u]) = klo[u];
+        *reinterpret_cast<u32x4*>(p.k_out + dout[u] + half) = khi[u];
+      }
+    }
+  }
+  if (p.status) {
+    const uint32_t any1 = __builtin_amdgcn_ballot_w64((bad & 1u) != 0) != 0 ? 1u : 0u;
+    const uint32_t any2 = __builtin_amdgcn_ballot_w64((bad & 2u) != 0) != 0 ? 2u : 0u;
+    if ((any1 | any2) && (threadIdx.x & 63) == 0) atomicOr(p.status, any1 | any2);
+  }
+}
+
+hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, int dtype, int D, hipStream_t stream) {
   if (B <= 0 || max_new <= 0) return hipSuccess;
+  (void)D;
+  if (p.rope.cos) {
+    const int64_t pairs = (int64_t)max_new * (p.cpr >> 1);
+    const int gx = (int)std::min<int64_t>(1024, (pairs + 256 * kRopeUnroll - 1) / (256 * kRopeUnroll));
+    if (dtype == 0)
+      hipLaunchKernelGGL(kv_append_rope_kernel<0>, dim3(gx, B), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL(kv_append_rope_kernel<1>, dim3(gx, B), dim3(256), 0, stream, p);
+    return hipGetLastError();
+  }
   // enough workgroups for one trip over the longest sequence, at most 1024 per sequence
   const int64_t chunks = (int64_t)max_new * p.cpr;
   const int gx = (int)std::min<int64_t>(1024, (chunks + 256 * kAppendUnroll - 1) / (256 * kAppendUnroll));

@@ -40,6 +40,7 @@
 #include <mutex>
 
 #include "kernels.hpp"
+#include "rope.hpp"
 
 namespace cie {
 
@@ -359,6 +360,12 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     for (int kk = 0; kk < C::KK; ++kk) qpre[e][kk] = load16(qrow + b * p.qs0 + 16 * kk + 8 * hl, rv && e < ne);
   }
   vm_wait<0>();
+  if (p.rope.cos) {  // RoPE fused into the load: row i at position ctx - Lq + i
+#pragma unroll
+    for (int e = 0; e < C::QPRE; ++e)
+      rope_q_lane<DTYPE, D>(qpre[e], p.rope.cos, p.rope.sin, p.rope.rows, (e < ne ? ent[e][1] : 0) - p.Lq + i,
+                            rv && e < ne, hl);
+  }
 #pragma unroll
   for (int e = 0; e < C::QPRE; ++e)
 #pragma unroll
@@ -402,10 +409,10 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
             for (int kk = 0; kk < C::KK; ++kk) qf[kk] = qpre[e][kk];
       } else {
 #pragma unroll
-        for (int kk = 0; kk < C::KK; ++kk) {
-          qf[kk] = load16(qrow + c_b * p.qs0 + 16 * kk + 8 * hl, rv);
-          qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
-        }
+        for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + c_b * p.qs0 + 16 * kk + 8 * hl, rv);
+        if (p.rope.cos) rope_q_lane<DTYPE, D>(qf, p.rope.cos, p.rope.sin, p.rope.rows, c_ctx - p.Lq + i, rv, hl);
+#pragma unroll
+        for (int kk = 0; kk < C::KK; ++kk) qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
       }
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};

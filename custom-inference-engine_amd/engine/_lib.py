@@ -34,6 +34,10 @@ EXPORTED_SYMBOLS = (
     "cie_paged_workspace_bytes",
     "cie_paged_fwd",
     "cie_kv_append",
+    "cie_rope_apply",
+    "cie_flash_fwd_rope",
+    "cie_paged_fwd_rope",
+    "cie_kv_append_rope",
 )
 
 
@@ -67,6 +71,20 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cie_kv_append.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]
     lib.cie_kv_append.restype = _i
+    lib.cie_rope_apply.argtypes = [_vp, _vp, _i64p, _i64p, _vp, ctypes.c_int64, _vp, _vp, _i, _vp,
+                                   _i, _i, _i, _i, _i, _vp]
+    lib.cie_rope_apply.restype = _i
+    lib.cie_flash_fwd_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
+                                       _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp, _vp, _i, _vp, _vp]
+    lib.cie_flash_fwd_rope.restype = _i
+    lib.cie_paged_fwd_rope.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                                       _i64p, _i64p, _i64p, _i64p,
+                                       _i, _i, _i, _i, _i, _i, _i, _i, _i,
+                                       ctypes.c_float, _i, _i, _vp, _vp, _i, _vp]
+    lib.cie_paged_fwd_rope.restype = _i
+    lib.cie_kv_append_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
+                                       _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i64p, _vp]
+    lib.cie_kv_append_rope.restype = _i
 
 
 def load() -> ctypes.CDLL:

@@ -46,12 +46,44 @@ def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
     return t.clone(memory_format=torch.contiguous_format)
 
 
+def _output(out: torch.Tensor | None, shape: tuple[int, ...], q: torch.Tensor) -> torch.Tensor:
+    """A new contiguous output, or the caller's after checking that the
+    kernels can write it in place."""
+    if out is None:
+        return torch.empty(shape, dtype=q.dtype, device=q.device)
+    if tuple(out.shape) != shape or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError(f"out must be {shape} {q.dtype} on {q.device}, got {tuple(out.shape)} {out.dtype}")
+    if _kernel_layout(out) is not out:
+        raise ValueError("out needs a unit last stride, 16-byte aligned rows and outer strides in multiples of 8")
+    return out
+
+
+def rope_args(rope: tuple[torch.Tensor, torch.Tensor], D: int, device: torch.device) -> tuple[int, int, int]:
+    """Validate RoPE tables (cos, sin: fp32 (rows, D/2), contiguous, on
+    ``device``, as ``RotaryEmbedding`` holds them) and return their
+    pointers and row count for the library."""
+    cos, sin = rope
+    for name, t in (("cos", cos), ("sin", sin)):
+        if not t.is_cuda or t.device != device:
+            raise RuntimeError(f"rope {name} table must be on {device}")
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != D // 2 or not t.is_contiguous():
+            raise ValueError(f"rope {name} table must be contiguous fp32 (rows, {D // 2}), got "
+                             f"{t.dtype} {tuple(t.shape)}")
+    if cos.shape != sin.shape or cos.shape[0] < 1:
+        raise ValueError(f"rope tables differ or are empty: {tuple(cos.shape)}, {tuple(sin.shape)}")
+    return cos.data_ptr(), sin.data_ptr(), int(cos.shape[0])
+
+
 def flash_attention(
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
     causal: bool = False,
     scale: float | None = None,
+    *,
+    rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+    q_pos0: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Flash attention on the GPU.
 
@@ -59,6 +91,14 @@ def flash_attention(
     head h reads kv head h // (H // Hk)). ``causal`` masks bottom-right
     aligned: row i sees keys j <= N - M + i. ``scale`` defaults to
     1/sqrt(D). Returns a new contiguous (B, H, M, D) tensor in q's dtype.
+
+    ``rope`` (keyword only, not in the reference's signature): (cos, sin)
+    tables; q is then un-rotated and row i of batch b is rotated at position
+    ``q_pos0[b] + i`` (int32 (B,) on the device; default 0) inside the
+    kernel, bit-identical to ``rope_apply`` on q first. k must already be
+    rotated. ``out``: an existing (B, H, M, D) tensor (any strides with a
+    unit last stride, e.g. the transposed view of a (B, M, H, D) buffer) to
+    write instead of a new one.
     """
     if not q.is_cuda:
         raise RuntimeError("flash_attention requires CUDA tensors")
@@ -82,13 +122,27 @@ def flash_attention(
 
     lib = _lib.load()
     q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
-    out = torch.empty((B, H, M, D), dtype=q.dtype, device=q.device)
+    out = _output(out, (B, H, M, D), q)
     with torch.cuda.device(q.device):
-        rc = lib.cie_flash_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-            _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
-            B, H, Hk, M, N, D, float(scale), 1 if causal else 0,
-            _lib.DTYPE_CODES[q.dtype], _lib.stream_handle(q.device))
+        if rope is None:
+            rc = lib.cie_flash_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
+                B, H, Hk, M, N, D, float(scale), 1 if causal else 0,
+                _lib.DTYPE_CODES[q.dtype], _lib.stream_handle(q.device))
+        else:
+            cos_p, sin_p, rows = rope_args(rope, D, q.device)
+            pos_p = None
+            if q_pos0 is not None:
+                if not q_pos0.is_cuda or q_pos0.device != q.device or q_pos0.dtype != torch.int32 \
+                        or q_pos0.shape != (B,) or not q_pos0.is_contiguous():
+                    raise ValueError("q_pos0 must be a contiguous int32 (B,) tensor on q's device")
+                pos_p = q_pos0.data_ptr()
+            rc = lib.cie_flash_fwd_rope(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
+                B, H, Hk, M, N, D, float(scale), 1 if causal else 0,
+                _lib.DTYPE_CODES[q.dtype], cos_p, sin_p, rows, pos_p, _lib.stream_handle(q.device))
     _lib.check(rc)
     return out
 
@@ -126,6 +180,9 @@ def paged_attention(
     scale: float | None = None,
     max_context: int | None = None,
     workspace: torch.Tensor | None = None,
+    *,
+    rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention of the newest ``Lq`` tokens of each sequence over its paged
     KV history.
@@ -142,6 +199,11 @@ def paged_attention(
     :func:`paged_workspace_bytes` bytes; by default a cached per-(device,
     stream) buffer is used. Equal to ``flash_attention`` over ``cache.gather``
     per sequence. Returns (B, Hq, Lq, D) in q's dtype.
+
+    ``rope``: (cos, sin) tables; q is then un-rotated and row i of sequence
+    b is rotated at position ``context_lens[b] - Lq + i`` as it is loaded,
+    bit-identical to ``rope_apply`` on q first. ``out``: an existing
+    (B, Hq, Lq, D) tensor to write, as in :func:`flash_attention`.
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_tables", block_tables), ("context_lens", context_lens)):
@@ -181,15 +243,16 @@ def paged_attention(
     elif not workspace.is_cuda or workspace.device != q.device:
         raise RuntimeError("paged_attention: workspace must be on the query's CUDA device")
     ws_have = workspace.numel() * workspace.element_size()
-    out = torch.empty((B, Hq, Lq, D), dtype=q.dtype, device=q.device)
-    with torch.cuda.device(q.device):
-        rc = lib.cie_paged_fwd(
-            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(),
-            out.data_ptr(),
-            workspace.data_ptr(),
-            ws_have,
+    out = _output(out, (B, Hq, Lq, D), q)
+    args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(),
+            out.data_ptr(), workspace.data_ptr(), ws_have,
             _lib.strides(q), _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out),
             B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc,
-            float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype], stream)
+            float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype])
+    with torch.cuda.device(q.device):
+        if rope is None:
+            rc = lib.cie_paged_fwd(*args, stream)
+        else:
+            rc = lib.cie_paged_fwd_rope(*args, *rope_args(rope, D, q.device), stream)
     _lib.check(rc)
     return out

@@ -15,7 +15,9 @@ Added for the paged kernels: :func:`block_table_tensor`, which packs host
 block tables into the int32 ``(B, max_blocks)`` / ``(B,)`` device format the
 kernels read; :func:`kv_append`, the batched device write of new tokens
 (``cie_kv_append``); :meth:`PagedKVCache.append_batch`, its per-layer use for
-many sequences; and :meth:`PagedKVCache.attend`, which runs
+many sequences; :meth:`PagedKVCache.prepare_step` / :meth:`append_step`,
+which upload a step's metadata once for all layers (:class:`StepBatch`);
+and :meth:`PagedKVCache.attend`, which runs
 ``paged_attention`` on one layer's pools. On a CUDA device ``append`` writes
 through ``cie_kv_append`` (the reference's per-block slice loop,
 kv_cache.py:128-136, becomes one launch); a cache on the CPU device keeps the
@@ -48,6 +50,38 @@ class KVCacheConfig:
         return 2 * self.num_layers * self.num_blocks * self.block_size * self.num_kv_heads * self.head_dim * elt
 
 
+@dataclass
+class StepBatch:
+    """Device-resident metadata of one engine step for B sequences
+    (:meth:`PagedKVCache.prepare_step`), read by every layer's append and
+    paged attention: int32 block tables (B, max_blocks), context lengths (B,)
+    including the step's new tokens, row offsets ``cu_new`` (B+1,) of the
+    new tokens (``num_new`` per sequence) and their start positions (B,).
+    ``max_context`` bounds ``context_lens``."""
+    block_tables: torch.Tensor
+    context_lens: torch.Tensor
+    cu_new: torch.Tensor
+    starts: torch.Tensor
+    num_new: int
+    max_context: int
+    tables: tuple = ()           # the host BlockTables, in batch order
+    starts_host: tuple = ()      # host copies of starts and context lengths
+    lengths_host: tuple = ()
+
+    @property
+    def fresh(self) -> bool:
+        """Every sequence holds exactly this step's tokens (a prefill from
+        position 0): attention needs only the new K/V, no history."""
+        return all(s0 == 0 and n == self.num_new for s0, n in zip(self.starts_host, self.lengths_host))
+
+    @property
+    def aligned(self) -> bool:
+        """The new tokens are the newest of every sequence (start + num_new
+        == context length), so their positions are context_len - num_new + i,
+        as the paged kernel's fused RoPE assumes."""
+        return all(s0 + self.num_new == n for s0, n in zip(self.starts_host, self.lengths_host))
+
+
 def block_table_tensor(
     tables: Sequence[BlockTable],
     device: torch.device | str,
@@ -72,7 +106,9 @@ def block_table_tensor(
 
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
               block_tables: torch.Tensor, cu_new: torch.Tensor, start: torch.Tensor,
-              max_new: int, status: torch.Tensor | None = None) -> None:
+              max_new: int, status: torch.Tensor | None = None, *,
+              rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+              k_out: torch.Tensor | None = None) -> None:
     """Write new tokens of B sequences into one layer's pools on the GPU.
 
     k_new / v_new: (T, Hk, D); the rows of sequence b are
@@ -80,8 +116,14 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v
     ``start[b] + i`` (int32 (B,), device) through ``block_tables`` (int32
     (B, max_blocks), device, already holding the needed blocks). ``max_new``
     bounds the per-sequence count. ``status`` (optional int32/uint32 (1,),
-    device) is set to 1 if a position or block id was out of range; those
+    device) gets 1 ORed in if a position or block id was out of range; those
     tokens are not written.
+
+    ``rope``: (cos, sin) tables; k_new is then un-rotated and each K row is
+    rotated at its position before it is written (bit-identical to
+    ``rope_apply`` on k first); a position outside the tables writes neither
+    K nor V of the token and ORs 2 into status. ``k_out`` (T, Hk, D) then
+    also receives the rotated rows.
     """
     from engine import _lib
 
@@ -108,13 +150,26 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v
     if k_new.stride(-1) != 1 or v_new.stride(-1) != 1:
         k_new, v_new = k_new.contiguous(), v_new.contiguous()
     lib = _lib.load()
-    with torch.cuda.device(k_cache.device):
-        rc = lib.cie_kv_append(
-            k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+    args = (k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
             _lib.strides3(k_new), _lib.strides3(v_new), _lib.strides(k_cache), _lib.strides(v_cache),
             bt.data_ptr(), cu.data_ptr(), st.data_ptr(), status.data_ptr() if status is not None else None,
-            B, k_new.shape[0], int(max_new), Hk, D, nb, bs, bt.shape[1],
-            _lib.DTYPE_CODES[k_cache.dtype], _lib.stream_handle(k_cache.device))
+            B, k_new.shape[0], int(max_new), Hk, D, nb, bs, bt.shape[1], _lib.DTYPE_CODES[k_cache.dtype])
+    if rope is None and k_out is not None:
+        raise ValueError("kv_append: k_out is only written together with rope")
+    with torch.cuda.device(k_cache.device):
+        if rope is None:
+            rc = lib.cie_kv_append(*args, _lib.stream_handle(k_cache.device))
+        else:
+            from engine.attention import rope_args
+
+            out_p, out_st = None, None
+            if k_out is not None:
+                if not k_out.is_cuda or k_out.device != k_cache.device or k_out.dtype != k_cache.dtype \
+                        or tuple(k_out.shape) != tuple(k_new.shape) or k_out.stride(-1) != 1:
+                    raise ValueError(f"kv_append: k_out must match k_new {tuple(k_new.shape)} on the pool's device")
+                out_p, out_st = k_out.data_ptr(), _lib.strides3(k_out)
+            rc = lib.cie_kv_append_rope(*args, *rope_args(rope, D, k_cache.device), out_p, out_st,
+                                        _lib.stream_handle(k_cache.device))
     _lib.check(rc)
 
 
@@ -206,19 +261,58 @@ class PagedKVCache:
                 done += n
         table.length = max(table.length, end)
 
-    def prepare_step(self, tables: Sequence[BlockTable], num_new: int, starts: Sequence[int] | None = None
-                     ) -> tuple[torch.Tensor, torch.Tensor]:
+    def prepare_step(self, tables: Sequence[BlockTable], num_new: int, starts: Sequence[int] | None = None,
+                     max_blocks: int | None = None) -> "StepBatch":
         """Host side of one engine step for a batch: allocate the blocks the
         ``num_new`` tokens of every sequence need (at ``starts[b]``, default
-        each table's end), extend the lengths, and return the int32 device
-        block table + context lengths that every layer's ``append_batch`` and
-        ``paged_attention`` of the step share (one host-to-device copy)."""
+        each table's end), extend the lengths, and upload everything the
+        step's kernels read (block tables, context lengths, the row offsets
+        and start positions of the new tokens) in ONE host-to-device copy.
+        Every layer's :meth:`append_step` and ``paged_attention`` of the step
+        reuses it, so no layer touches the host."""
+        if self.device.type != "cuda":
+            raise RuntimeError("prepare_step requires a CUDA cache")
         starts = [t.length for t in tables] if starts is None else list(starts)
+        if len(starts) != len(tables) or num_new < 0 or any(s < 0 for s in starts):
+            raise ValueError(f"bad step: {len(tables)} tables, starts {starts}, num_new {num_new}")
         for t, s0 in zip(tables, starts):
             while len(t.blocks) < t.num_blocks_needed(s0 + num_new):
                 t.blocks.append(self._alloc_block())
             t.length = max(t.length, s0 + num_new)
-        return block_table_tensor(tables, self.device)
+        B = len(tables)
+        width = max([len(t.blocks) for t in tables] + [1]) if max_blocks is None else max_blocks
+        host = torch.zeros(B * width + 3 * B + 1, dtype=torch.int32)
+        for i, t in enumerate(tables):
+            if len(t.blocks) > width:
+                raise ValueError(f"sequence {i} holds {len(t.blocks)} blocks, more than max_blocks={width}")
+            if t.blocks:
+                host[i * width:i * width + len(t.blocks)] = torch.tensor(t.blocks, dtype=torch.int32)
+        o = B * width
+        host[o:o + B] = torch.tensor([t.length for t in tables], dtype=torch.int32)
+        host[o + B:o + 2 * B + 1] = torch.arange(B + 1, dtype=torch.int32) * num_new
+        host[o + 2 * B + 1:] = torch.tensor(starts, dtype=torch.int32)
+        dev = host.to(self.device)
+        lengths = tuple(t.length for t in tables)
+        return StepBatch(block_tables=dev[:o].view(B, width), context_lens=dev[o:o + B],
+                         cu_new=dev[o + B:o + 2 * B + 1], starts=dev[o + 2 * B + 1:], num_new=num_new,
+                         max_context=max(lengths + (1,)), tables=tuple(tables), starts_host=tuple(starts),
+                         lengths_host=lengths)
+
+    def append_step(self, layer: int, step: "StepBatch", k: torch.Tensor, v: torch.Tensor, *,
+                    rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+                    k_out: torch.Tensor | None = None) -> None:
+        """Write one layer's new K/V rows of a prepared step: k, v are
+        (B * num_new, Hk, D), the rows of sequence b consecutive. One
+        ``cie_kv_append`` launch; no host work, no host-to-device copy, so a
+        step's layers can be captured in one HIP graph. ``rope`` / ``k_out``
+        as in :func:`kv_append` (K rotated at its position on the way in)."""
+        self._validate(k)
+        self._validate(v)
+        B = step.context_lens.shape[0]
+        if k.shape[0] != B * step.num_new or v.shape[0] != k.shape[0]:
+            raise ValueError(f"append_step expects {B * step.num_new} rows, got {k.shape[0]}, {v.shape[0]}")
+        kv_append(k, v, self.k[layer], self.v[layer], step.block_tables, step.cu_new, step.starts,
+                  max_new=step.num_new, rope=rope, k_out=k_out)
 
     def append_batch(self, layer: int, tables: Sequence[BlockTable], k: torch.Tensor, v: torch.Tensor,
                      lengths: Sequence[int], starts: Sequence[int] | None = None,

@@ -12,6 +12,10 @@
  *                   engine/model/block.py:56-71 (cache.gather at
  *                   engine/cache/kv_cache.py:141-165 followed by flash_attention).
  *
+ * Around them: cie_kv_append (the pool write of new tokens), cie_rope_apply
+ * (rotary embedding) and the _rope variants that fuse the rotation into the
+ * append and the query loads.
+ *
  * Conventions shared by every entry point:
  *   - Every pointer is a device pointer (e.g. torch.Tensor.data_ptr()).
  *   - Strides are in elements, four per tensor, outermost first. The innermost
@@ -126,9 +130,9 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
  *        new tokens need); start: int32 [B], position of each sequence's first
  *        new token; token i of sequence b goes to position start[b] + i
  *   max_new: an upper bound of cu_new[b+1] - cu_new[b] (sizes the launch)
- *   status: optional uint32 on the device, set to 1 when a position falls
- *        outside the table or a block id outside [0, num_blocks) (such tokens
- *        are not written); may be NULL
+ *   status: optional uint32 on the device; 1 is ORed into it when a position
+ *        falls outside the table or a block id outside [0, num_blocks) (such
+ *        tokens are not written); may be NULL
  * Reference: the per-block slice loop of PagedKVCache.append,
  * engine/cache/kv_cache.py:128-136 (block allocation, :122-125, stays on the
  * host), with the block ids read on the device instead of copied per call
@@ -140,6 +144,96 @@ int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
                   const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
                   uint32_t* status, int B, int T, int max_new, int Hk, int D,
                   int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream);
+
+/*
+ * Rotary position embedding (RoPE).
+ *
+ * rope_cos, rope_sin: fp32 device tables of shape (rope_rows, D/2), row-major
+ * and 16-byte aligned: RotaryEmbedding's cos / sin buffers
+ * (engine/model/rope.py:12-16, built by kernels/ref/rope_apply_ref.py:6-19).
+ * Every entry point below rotates exactly as apply_rotary_ref
+ * (kernels/ref/rope_apply_ref.py:46-53): x1 = x[:D/2], x2 = x[D/2:],
+ * rot1 = x1*c - x2*s, rot2 = x1*s + x2*c with each product, difference and
+ * sum rounded to fp32 (no fused multiply-add) and the result rounded to the
+ * element type, so its output is bit-identical to the reference's.
+ */
+
+/*
+ * out = RoPE(x): x, out (B, H, L, D) (out may be x). positions: int32 on the
+ * device, position of row l of batch b = positions[b * pos_batch_stride + l]
+ * (pos_batch_stride 0: one (L,) vector for every batch, as
+ * apply_rotary_ref's 1-d positions; L: a (B, L) matrix), or NULL for 0..L-1
+ * (the reference's default). A position outside [0, rope_rows) makes its row
+ * NaN and ORs 2 into *status (optional device uint32), where the
+ * reference's table indexing raises.
+ * Reference: RotaryEmbedding.apply (engine/model/rope.py:18-19) ->
+ * apply_rotary_ref (kernels/ref/rope_apply_ref.py:22-53).
+ */
+int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int64_t* out_stride,
+                   const int32_t* positions, int64_t pos_batch_stride,
+                   const float* rope_cos, const float* rope_sin, int rope_rows,
+                   uint32_t* status, int B, int H, int L, int D, int dtype, void* stream);
+
+/*
+ * cie_flash_fwd with RoPE fused into the query load: q holds the projected,
+ * un-rotated queries; row i of batch b is rotated at position q_pos0[b] + i
+ * (q_pos0: int32 [B] on the device, or NULL for position i) before the
+ * scores are formed. k must already be rotated (cie_kv_append_rope writes a
+ * dense rotated copy for this). The result is bit-identical to
+ * cie_rope_apply on q followed by cie_flash_fwd. A row whose position is
+ * outside [0, rope_rows) is NaN.
+ * Reference: engine/model/block.py:53-54 (q = rope.apply(q, positions))
+ * followed by the attention call of block.py:69-71.
+ */
+int cie_flash_fwd_rope(const void* q, const void* k, const void* v, void* o,
+                       const int64_t* q_stride, const int64_t* k_stride,
+                       const int64_t* v_stride, const int64_t* o_stride,
+                       int B, int Hq, int Hk, int Lq, int Lk, int D,
+                       float scale, int causal, int dtype,
+                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const int32_t* q_pos0, void* stream);
+
+/*
+ * cie_paged_fwd with RoPE fused into the query load: query row i of sequence
+ * b is rotated at position context_lens[b] - Lq + i, the position of that
+ * token in the sequence (the same alignment the causal mask uses; the
+ * engine's positions, arange(start, start + Lq) with start + Lq the context
+ * length, engine/model/transformer.py:35-37). Bit-identical to cie_rope_apply
+ * on q followed by cie_paged_fwd. A row whose position is outside
+ * [0, rope_rows) is NaN.
+ * Reference: engine/model/block.py:53 followed by block.py:65-71.
+ */
+int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* block_tables, const int32_t* context_lens,
+                       void* o, void* workspace, size_t workspace_bytes,
+                       const int64_t* q_stride, const int64_t* kc_stride,
+                       const int64_t* vc_stride, const int64_t* o_stride,
+                       int B, int Hq, int Hk, int Lq, int D,
+                       int num_blocks, int block_size, int max_blocks_per_seq,
+                       int max_context, float scale, int causal, int dtype,
+                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       void* stream);
+
+/*
+ * cie_kv_append with RoPE fused into the write of K: k_new holds the
+ * projected, un-rotated keys; token i of sequence b is rotated at position
+ * start[b] + i, then written (V is copied as is). k_out (optional, may be
+ * NULL; k_out_stride: strides of its (T, Hk, D) layout) receives the rotated
+ * K rows as well, for attention over the new tokens themselves (prefill).
+ * A position outside [0, rope_rows) writes neither K nor V of that token and
+ * ORs 2 into *status; positions outside the block table OR in 1 as in
+ * cie_kv_append.
+ * Reference: engine/model/block.py:54 (k = rope.apply(k, positions))
+ * followed by the append of block.py:57-64 -> kv_cache.py:128-136.
+ */
+int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const int64_t* new_stride, const int64_t* v_new_stride,
+                       const int64_t* kc_stride, const int64_t* vc_stride,
+                       const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
+                       uint32_t* status, int B, int T, int max_new, int Hk, int D,
+                       int num_blocks, int block_size, int max_blocks_per_seq, int dtype,
+                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       void* k_out, const int64_t* k_out_stride, void* stream);
 
 #ifdef __cplusplus
 }

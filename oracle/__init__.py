@@ -13,12 +13,15 @@ Contents
                    composition (``engine/cache/kv_cache.py:141-165`` gather,
                    ``engine/cache/block_table.py:23-26`` block math) and the
                    append loop (``engine/cache/kv_cache.py:128-136``).
+``rope_ref``       fp32 torch restatement of the reference's rotary tables
+                   and rotation (``kernels/ref/rope_apply_ref.py:6-53``).
 ``brute``          fp64 numpy brute force written independently of the
                    above (explicit per-row max-subtracted exponentials).
 
 Pinning: every function here is checked in ``tests/test_oracle.py`` against
 the reference's own known answers (``tests/kernels/test_flash_attention_ref.py``,
-``tests/cache/test_block_table.py``), against the fp64 brute force, against
+``tests/cache/test_block_table.py``, ``tests/kernels/test_rope_ref.py``,
+``tests/model/test_rope.py``), against the fp64 brute force, against
 ``torch.nn.functional.scaled_dot_product_attention`` with an explicit
 bottom-right mask, against closed-form special cases, and against planted
 mistakes that those checks must catch. No function is "parity unpinned".
@@ -34,3 +37,4 @@ from oracle.attention_ref import (  # noqa: F401
     paged_attention_ref,
 )
 from oracle.brute import attention_brute_f64, paged_attention_brute_f64  # noqa: F401
+from oracle.rope_ref import build_rope_cache_ref, rope_ref  # noqa: F401

@@ -192,7 +192,7 @@ def test_attention_section_matches_reference_per_sequence_path(L, dtype):
     k = torch.randn(B, Hk, L, D, generator=g).to(dtype)
     v = torch.randn(B, Hk, L, D, generator=g).to(dtype)
     step = cache.prepare_step(tables, L, starts)
-    out = attention_section(q.to(DEV), k.to(DEV), v.to(DEV), 1, cache, tables, starts, step)
+    out = attention_section(q.to(DEV), k.to(DEV), v.to(DEV), 1, cache, step)
     assert out.shape == (B, L, Hq * D)
     tol = 2e-3 if dtype == torch.float16 else 1e-2
     for b, t in enumerate(tables):
