@@ -25,7 +25,9 @@ The same line carries
                 step (batched append + paged attention; eager, HIP-graph
                 replay, with RoPE fused or applied first) beside the
                 reference's per-sequence append / gather / dense
-                structure; and the S=16384 D=128 bf16 prefill in TFLOP/s.
+                structure; the INT8-weight GEMM at the reference's
+                benchmark shapes (64 and 512 x 4096 x 4096) in TFLOP/s and
+                GB/s; and the S=16384 D=128 bf16 prefill in TFLOP/s.
 """
 
 from __future__ import annotations
@@ -232,6 +234,38 @@ class RopeLaunch:
     def __call__(self, i=0):
         t = self.bufs[i % self.copies]
         rc = self.lib.cie_rope_apply(t.data_ptr(), t.data_ptr(), *self.tail)
+        if rc:
+            from engine import _lib
+            _lib.check(rc)
+
+
+class Int8Launch:
+    """Pre-bound cie_int8_matmul at the reference's benchmark shapes
+    (benchmarks/bench_int8_matmul.py:14: M x 4096 x 4096, fp16 activations,
+    per-channel fp16 scales), rotating over weight copies that together
+    exceed `min_bytes` so the Infinity Cache cannot hold them."""
+
+    def __init__(self, M, dev, N=4096, K=4096, min_bytes=512 << 20):
+        import torch
+        from engine import _lib
+
+        self.lib = _lib.load()
+        g = torch.Generator().manual_seed(12)
+        w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+        self.copies = max(1, -(-min_bytes // (N * K)))
+        self.ws_ = [w.to(dev) for _ in range(self.copies)]
+        self.x = torch.randn(M, K, generator=g).half().to(dev)
+        self.s = (torch.rand(N, generator=g) * 0.01).half().to(dev)
+        self.y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        nbytes = int(self.lib.cie_int8_matmul_workspace_bytes(M, N, K))
+        self.work = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        self.args_tail = (self.s.data_ptr(), None, self.y.data_ptr(), K, K, N, M, N, K, 0, 0,
+                          self.work.data_ptr(), self.work.numel(), _lib.stream_handle(dev))
+        self.flops = 2.0 * M * N * K
+        self.bytes = N * K + M * K * 2 + M * N * 2 + N * 2  # weights, x, y, scales: each once
+
+    def __call__(self, i=0):
+        rc = self.lib.cie_int8_matmul(self.x.data_ptr(), self.ws_[i % self.copies].data_ptr(), *self.args_tail)
         if rc:
             from engine import _lib
             _lib.check(rc)
@@ -494,6 +528,16 @@ def main():
                                             "dtype": "fp16"}
         del rl
         extra["prefill_section_b4_s2048_rope"] = prefill_section_times(dev)
+        for M in (64, 512):
+            il = Int8Launch(M, dev)
+            ms = event_time_ms(il, max(50, 4 * il.copies), il.copies)
+            gbs = il.bytes / (ms / 1e3) / 1e9
+            tfs = il.flops / (ms / 1e3) / 1e12
+            extra[f"int8_matmul_m{M}_n4096_k4096"] = {
+                "us": round(ms * 1e3, 2), "TFLOP/s": round(tfs, 2), "frac_mfma": round(tfs / PEAK_MFMA_F16_TFLOPS, 4),
+                "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": il.copies,
+                "dtype": "fp16 x int8"}
+            del il
         extra["decode_step_b32_one_layer"] = decode_step_times(dev)
         c5 = workloads.prefill_s16384()
         f5 = FlashLaunch(c5, dev)

@@ -404,6 +404,63 @@ int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void
                      stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, k_out, k_out_stride);
 }
 
+size_t cie_int8_matmul_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return cie::int8_gemm_geometry(M, N, K).workspace_bytes;
+}
+
+int cie_int8_matmul(const void* x, const int8_t* w, const void* scales, const void* bias, void* y,
+                    int64_t x_row_stride, int64_t w_row_stride, int64_t y_row_stride,
+                    int M, int N, int K, int dtype, int scale_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype != CIE_DTYPE_F16 && dtype != CIE_DTYPE_BF16)
+    return fail(CIE_EDTYPE, "unsupported activation dtype code %d (f16 = 0, bf16 = 1)", dtype);
+  if (scale_dtype < 0 || scale_dtype > 2)
+    return fail(CIE_EDTYPE, "unsupported scale dtype code %d (f16 = 0, bf16 = 1, f32 = 2)", scale_dtype);
+  if (M < 0 || N < 0 || K < 0) return fail(CIE_EINVAL, "negative size (M=%d, N=%d, K=%d)", M, N, K);
+  if (K % 64) return fail(CIE_EINVAL, "in_features K=%d must be a multiple of 64", K);
+  if ((int64_t)M * N == 0) {
+    g_err.clear();
+    return CIE_OK;
+  }
+  if (K == 0) return fail(CIE_EINVAL, "in_features K must be positive");
+  CIE_TRY(check_ptr("x", x));
+  CIE_TRY(check_ptr("w_int8", w));
+  if (!y || reinterpret_cast<uintptr_t>(y) % 8) return fail(CIE_EINVAL, "y: NULL or not 8-byte aligned");
+  if (!scales) return fail(CIE_EINVAL, "scales: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(scales) % (scale_dtype == 2 ? 4 : 2))
+    return fail(CIE_EINVAL, "scales: pointer is not aligned to its element size");
+  if (bias && reinterpret_cast<uintptr_t>(bias) % 2) return fail(CIE_EINVAL, "bias: misaligned pointer");
+  if (x_row_stride < K || x_row_stride % 8)
+    return fail(CIE_EINVAL, "x row stride %lld must be >= K and a multiple of 8 elements", (long long)x_row_stride);
+  if (w_row_stride < K || w_row_stride % 16)
+    return fail(CIE_EINVAL, "w_int8 row stride %lld must be >= K and a multiple of 16 bytes",
+                (long long)w_row_stride);
+  if (y_row_stride < N) return fail(CIE_EINVAL, "y row stride %lld must be >= N", (long long)y_row_stride);
+  const cie::I8Geom g = cie::int8_gemm_geometry(M, N, K);
+  if ((int64_t)g.n_tiles * g.m_tiles * g.splits > 0x7fffffff) return fail(CIE_EINVAL, "problem too large");
+  if (g.workspace_bytes) {
+    if (!workspace || workspace_bytes < g.workspace_bytes)
+      return fail(CIE_EWORKSPACE, "workspace of %zu bytes required, %zu given", g.workspace_bytes,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(CIE_EINVAL, "workspace: pointer is not 16-byte aligned");
+  }
+  cie::I8GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.w = w;
+  p.scales = scales;
+  p.bias = static_cast<const uint16_t*>(bias);
+  p.y = static_cast<uint16_t*>(y);
+  p.partial = static_cast<float*>(workspace);
+  p.xs = x_row_stride;
+  p.wsr = w_row_stride;
+  p.ys = y_row_stride;
+  p.M = M; p.N = N; p.K = K; p.scale_dtype = scale_dtype;
+  p.n_tiles = g.n_tiles; p.m_tiles = g.m_tiles; p.splits = g.splits; p.ksteps = g.ksteps;
+  p.m_pad = g.m_pad; p.n_pad = g.n_pad;
+  return launch_status(cie::launch_int8_gemm(p, g, dtype, static_cast<hipStream_t>(stream)));
+}
+
 int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int64_t* out_stride,
                    const int32_t* positions, int64_t pos_batch_stride,
                    const float* rope_cos, const float* rope_sin, int rope_rows,

@@ -1,0 +1,381 @@
+// INT8-weight GEMM for gfx950: y = (x . w^T) * s[n] (+ bias[n]), x fp16/bf16
+// (M, K), w int8 (N, K) with per-output-channel scales s (N,), y (M, N) in x's
+// dtype. Replaces the Triton dequant-on-load kernel behind Int8Linear
+// (kernels/int8_matmul.py:16-62, wrapper :65-110, caller
+// engine/quant/int8_linear.py:37-41).
+//
+// Arithmetic. int8 values are exact in fp16 and bf16, so the weights are
+// converted in registers (fp16: byte | 0x6400 is 1024 + byte, minus 1152;
+// bf16: byte -> f32 -> bf16) and multiplied against x on the matrix cores
+// (v_mfma_f32_32x32x16_{f16,bf16}) with fp32 accumulation: the products are
+// exact, as in the reference, which up-casts both operands to fp32 before
+// tl.dot (:47-53). The scale multiplies the fp32 sum once per output
+// (:56-57) and the result is rounded to x's dtype; the bias is added after
+// that rounding, in x's dtype, as the wrapper does (:107-109).
+//
+// Tiling. A workgroup of 4 waves owns 128 weight rows (32 per wave, one MFMA
+// row tile) and BM = 32 * MT activation rows, and walks its K range in steps
+// of 64. Each step's x tile (BM x 64, 128-byte rows) and w tile (128 x 64,
+// 64-byte rows) are copied global -> LDS with direct-to-LDS loads into a
+// ring of NST stages, 16-byte chunks XOR-swizzled per row so that the
+// fragment reads below are bank-conflict free. The MFMA operands use a fixed
+// permutation of the contraction axis: for a 32-wide k group, lane (r, h)
+// (r = lane % 32, h = lane / 32) takes w[n_r][16h .. 16h+16) -- one 16-byte
+// fragment read -- whose first 8 values feed MFMA 0 and last 8 MFMA 1; the
+// x operand takes x[m_r][16h .. 16h+16) split the same way, so MFMA 0
+// contracts k in {0..7, 16..23} and MFMA 1 k in {8..15, 24..31}.
+//
+// Split K. When the (n, m) tiles alone cannot occupy the GPU (small M:
+// decode), the K steps are cut into `splits` contiguous ranges; each
+// workgroup writes its fp32 partial tile to the workspace in lane order
+// (16 contiguous bytes per lane, 1 KiB per wave instruction) and a second
+// kernel sums the partials of every output in split order (deterministic),
+// scales, rounds and adds the bias. (Folding that sum into the last
+// workgroup to finish a tile needs device-coherent stores, an arrival
+// atomic and coherent reloads in series; on MI355X that chain cost more than
+// the second launch.)
+#include <mutex>
+
+#include "kernels.hpp"
+
+namespace cie {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kI8BN = 128;  // weight rows per workgroup
+constexpr int kI8BK = 64;   // k per step
+constexpr int kI8MaxSplitTiles = 256;  // K is split only when there are fewer (n, m) tiles
+
+constexpr int kI8MaxSplits = 16;
+
+template <int MT, int NST_>
+struct I8Cfg {
+  static constexpr int BM = 32 * MT;
+  static constexpr int NST = NST_;  // LDS ring stages
+  static constexpr int X_BYTES = BM * kI8BK * 2;        // x tile per stage
+  static constexpr int W_BYTES = kI8BN * kI8BK;         // w tile per stage
+  static constexpr int STAGE = X_BYTES + W_BYTES;
+  static constexpr int XI = X_BYTES / (256 * 16);       // x copies per lane per stage
+  static constexpr int WI = W_BYTES / (256 * 16);       // w copies per lane per stage
+  static constexpr int PER = XI + WI;
+  static_assert(XI >= 1 && WI == 2, "tile must split over 4 waves");
+  static_assert(PER * (NST - 1) < 64, "vmcnt range");
+};
+
+// 16 int8 -> two groups of 8 fp16 / bf16 (u32x4 each), exact.
+template <int DTYPE> __device__ __forceinline__ void dequant16(u32x4 q, u32x4& a0, u32x4& a1);
+
+template <> __device__ __forceinline__ void dequant16<0>(u32x4 q, u32x4& a0, u32x4& a1) {
+  uint32_t o[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t u = q[d] ^ 0x80808080u;  // byte b -> b + 128
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 0x64 u1 0x64 u0
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 0x64 u3 0x64 u2
+    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) - bias);
+    o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) - bias);
+  }
+  a0 = u32x4{o[0], o[1], o[2], o[3]};
+  a1 = u32x4{o[4], o[5], o[6], o[7]};
+}
+
+template <> __device__ __forceinline__ void dequant16<1>(u32x4 q, u32x4& a0, u32x4& a1) {
+  uint32_t o[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t u = q[d] ^ 0x80808080u;
+    const float f0 = (float)(u & 0xffu) - 128.0f, f1 = (float)((u >> 8) & 0xffu) - 128.0f;
+    const float f2 = (float)((u >> 16) & 0xffu) - 128.0f, f3 = (float)(u >> 24) - 128.0f;
+    o[2 * d] = Elt<1>::pack2(f0, f1);
+    o[2 * d + 1] = Elt<1>::pack2(f2, f3);
+  }
+  a0 = u32x4{o[0], o[1], o[2], o[3]};
+  a1 = u32x4{o[4], o[5], o[6], o[7]};
+}
+
+template <int DTYPE>
+__device__ __forceinline__ float elt_to_f32(uint16_t h) {
+  if constexpr (DTYPE == 0) return (float)__builtin_bit_cast(_Float16, h);
+  else return __uint_as_float((uint32_t)h << 16);
+}
+
+__device__ __forceinline__ float load_scale(const void* s, int n, int sdtype) {
+  if (sdtype == 2) return static_cast<const float*>(s)[n];
+  const uint16_t h = static_cast<const uint16_t*>(s)[n];
+  return sdtype == 0 ? (float)__builtin_bit_cast(_Float16, h) : __uint_as_float((uint32_t)h << 16);
+}
+
+// y = round(acc * s) (+ bias, rounded again), for 4 consecutive outputs.
+template <int DTYPE>
+__device__ __forceinline__ u32x2 finish4(const float (&a)[4], const I8GemmParams& p, int n) {
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int ne = min(n + e, p.N - 1);
+    float t = a[e] * load_scale(p.scales, ne, p.scale_dtype);
+    if (p.bias) {
+      // the reference adds the bias to the rounded product, in the output dtype
+      const uint32_t r = Elt<DTYPE>::pack2(t, 0.f);
+      t = elt_to_f32<DTYPE>((uint16_t)r) + elt_to_f32<DTYPE>(p.bias[ne]);
+    }
+    v[e] = t;
+  }
+  return u32x2{Elt<DTYPE>::pack2(v[0], v[1]), Elt<DTYPE>::pack2(v[2], v[3])};
+}
+
+template <int DTYPE>
+__device__ __forceinline__ void store4(const I8GemmParams& p, int m, int n, u32x2 pk) {
+  if (m >= p.M || n >= p.N) return;
+  uint16_t* dst = p.y + (int64_t)m * p.ys + n;
+  if (n + 3 < p.N && (p.ys & 3) == 0) {  // 8-byte aligned (n is a multiple of 4)
+    *reinterpret_cast<u32x2*>(dst) = pk;
+  } else {
+    const uint16_t h[4] = {(uint16_t)pk[0], (uint16_t)(pk[0] >> 16), (uint16_t)pk[1], (uint16_t)(pk[1] >> 16)};
+    for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = h[e];
+  }
+}
+
+// vm_wait for the copies of `ahead` k steps issued after the one needed (uniform `ahead`)
+template <int PER, int MAXA>
+__device__ __forceinline__ void wait_steps_ahead(int ahead) {
+  if constexpr (MAXA > 0) {
+    if (ahead >= MAXA) {
+      vm_wait<MAXA * PER>();
+      return;
+    }
+    wait_steps_ahead<PER, MAXA - 1>(ahead);
+  } else {
+    vm_wait<0>();
+  }
+}
+
+template <int DTYPE, int MT, int NST>
+__global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p) {
+  using C = I8Cfg<MT, NST>;
+  using E = Elt<DTYPE>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  // tile order: the m tiles of one weight tile are consecutive logical ids,
+  // and consecutive logical ids land on one XCD (round-robin dispatch), so a
+  // weight tile read by several m tiles is shared through that XCD's L2
+  const int NWG = p.n_tiles * p.m_tiles * p.splits;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int logical = xcd * (NWG >> 3) + min(xcd, NWG & 7) + slot;
+  const int split = logical % p.splits;
+  const int rest = logical / p.splits;
+  const int mt_i = rest % p.m_tiles;
+  const int nt_i = rest / p.m_tiles;
+  const int n0 = nt_i * kI8BN, m0 = mt_i * C::BM;
+  const int ks0 = (int)((int64_t)split * p.ksteps / p.splits);
+  const int ks1 = (int)((int64_t)(split + 1) * p.ksteps / p.splits);
+  const int T = ks1 - ks0;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r32 = lane & 31, hk = lane >> 5;
+  const uint32_t lds0 = lds_addr_of(smem);
+
+  // per-lane copy sources (row clamped into the tensor; rows past M / N are
+  // computed but never stored)
+  const uint8_t* xsrc[C::XI];
+  uint32_t xdst[C::XI];
+#pragma unroll
+  for (int j = 0; j < C::XI; ++j) {
+    const int P = (j * 4 + w) * 64 + lane;  // x chunk slot in the tile: 8 per row
+    const int r = P >> 3, c = (P & 7) ^ chunk_swizzle<8>(r);
+    const int m = min(m0 + r, p.M - 1);
+    xsrc[j] = reinterpret_cast<const uint8_t*>(p.x + (int64_t)m * p.xs + 8 * c);
+    xdst[j] = (uint32_t)((j * 4 + w) * 64 * 16);
+  }
+  const uint8_t* wsrc[C::WI];
+  uint32_t wdst[C::WI];
+#pragma unroll
+  for (int j = 0; j < C::WI; ++j) {
+    const int P = (j * 4 + w) * 64 + lane;  // w chunk slot: 4 per row
+    const int r = P >> 2, c = (P & 3) ^ chunk_swizzle<4>(r);
+    const int n = min(n0 + r, p.N - 1);
+    wsrc[j] = reinterpret_cast<const uint8_t*>(p.w) + (int64_t)n * p.wsr + 16 * c;
+    wdst[j] = (uint32_t)(C::X_BYTES + (j * 4 + w) * 64 * 16);
+  }
+  auto issue = [&](int t) {
+    const uint32_t st = lds0 + (uint32_t)((t % C::NST) * C::STAGE);
+    const int64_t kx = (int64_t)(ks0 + t) * kI8BK * 2;  // bytes into an x row
+    const int64_t kw = (int64_t)(ks0 + t) * kI8BK;      // bytes into a w row
+#pragma unroll
+    for (int j = 0; j < C::XI; ++j) dma16_at(xsrc[j] + kx, st + xdst[j]);
+#pragma unroll
+    for (int j = 0; j < C::WI; ++j) dma16_at(wsrc[j] + kw, st + wdst[j]);
+  };
+
+  // fragment read offsets within a stage (bytes)
+  uint32_t woff[2], xoff[MT][2][2];
+  {
+    const int r = w * 32 + r32;
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) woff[g2] = C::X_BYTES + r * 64 + 16 * ((2 * g2 + hk) ^ chunk_swizzle<4>(r));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int rx = mt * 32 + r32;
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) xoff[mt][g2][g] = rx * 128 + 16 * ((4 * g2 + 2 * hk + g) ^ chunk_swizzle<8>(rx));
+    }
+  }
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+
+  const int pro = min(C::NST - 1, T);
+  for (int t = 0; t < pro; ++t) issue(t);
+  for (int t = 0; t < T; ++t) {
+    if (t + C::NST - 1 < T) issue(t + C::NST - 1);
+    wait_steps_ahead<C::PER, C::NST - 1>(min(C::NST - 1, T - 1 - t));  // steps issued after step t
+    __syncthreads();  // step t is in LDS for every wave
+    const uint8_t* st = smem + (t % C::NST) * C::STAGE;
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const u32x4 q = *reinterpret_cast<const u32x4*>(st + woff[g2]);
+      u32x4 a0, a1;
+      dequant16<DTYPE>(q, a0, a1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(st + xoff[mt][g2][0]);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(st + xoff[mt][g2][1]);
+        acc[mt] = E::mfma(a0, b0, acc[mt]);
+        acc[mt] = E::mfma(a1, b1, acc[mt]);
+      }
+    }
+    __syncthreads();  // every wave is done with the slot before it is refilled
+  }
+
+  // C[i][j] of a 32x32 tile: lane j + 32 * ((i / 4) % 2), element (i / 8) * 4 + i % 4;
+  // here i = weight row (n), j = activation row (m)
+  if (p.splits == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 32 + r32;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = w * 32 + 8 * q + 4 * hk;  // first of 4 consecutive rows in the tile
+        const float a[4] = {acc[mt][4 * q], acc[mt][4 * q + 1], acc[mt][4 * q + 2], acc[mt][4 * q + 3]};
+        store4<DTYPE>(p, m, n0 + nl, finish4<DTYPE>(a, p, n0 + nl));
+      }
+    }
+    return;
+  }
+
+  // partial tile in lane order: slot (split, tile, wave, mt, q, lane) holds
+  // the lane's 4 sums as 16 contiguous bytes (MT * 16 KiB per (split, tile))
+  const int tile = nt_i * p.m_tiles + mt_i;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    if (m0 + mt * 32 + r32 >= p.M) continue;  // rows past M are never summed
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t slot = (((((int64_t)split * p.n_tiles * p.m_tiles + tile) * 4 + w) * MT + mt) * 4 + q) * 64 + lane;
+      *reinterpret_cast<f32x4_t*>(p.partial + 4 * slot) =
+          f32x4_t{acc[mt][4 * q], acc[mt][4 * q + 1], acc[mt][4 * q + 2], acc[mt][4 * q + 3]};
+    }
+  }
+}
+
+// One thread per (tile, wave, mt, q, lane) slot of the partial layout: the
+// same 4 outputs that lane held in the main kernel, summed over the splits in
+// split order, then scaled, rounded and stored.
+template <int DTYPE, int MT>
+__global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParams p) {
+  const int64_t per_split = (int64_t)p.n_tiles * p.m_tiles * 4 * MT * 4 * 64;  // tiles x waves x MT x q x lanes
+  const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (slot >= per_split) return;
+  const int lane = (int)(slot & 63);
+  const int64_t r = slot >> 6;
+  const int q = (int)(r & 3);
+  const int mt = (int)((r >> 2) % MT);
+  const int64_t r3 = (r >> 2) / MT;
+  const int w = (int)(r3 & 3), tile = (int)(r3 >> 2);
+  const int mt_i = tile % p.m_tiles, nt_i = tile / p.m_tiles;
+  const int m = mt_i * 32 * MT + mt * 32 + (lane & 31);
+  const int n = nt_i * kI8BN + w * 32 + 8 * q + 4 * (lane >> 5);
+  if (m >= p.M) return;
+  f32x4_t v[kI8MaxSplits];  // every split's partial in flight at once
+#pragma unroll
+  for (int sp = 0; sp < kI8MaxSplits; ++sp)
+    if (sp < p.splits) v[sp] = *reinterpret_cast<const f32x4_t*>(p.partial + 4 * (sp * per_split + slot));
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < kI8MaxSplits; ++sp) {
+    if (sp < p.splits) {
+      a[0] += v[sp][0];
+      a[1] += v[sp][1];
+      a[2] += v[sp][2];
+      a[3] += v[sp][3];
+    }
+  }
+  store4<DTYPE>(p, m, n, finish4<DTYPE>(a, p, n));
+}
+
+I8Geom int8_gemm_geometry(int M, int N, int K) {
+  I8Geom g{};
+  g.n_tiles = (N + kI8BN - 1) / kI8BN;
+  g.ksteps = K / kI8BK;
+  // activation tile: 32 / 64 rows for small M, 128 when that still gives one
+  // (n, m) tile per CU
+  if (M <= 32) g.mt = 1;
+  else if (M <= 64) g.mt = 2;
+  else g.mt = (int64_t)g.n_tiles * ((M + 127) / 128) >= 256 ? 4 : 2;
+  // a single activation tile (decode): the weights stream through, so a deep
+  // ring keeps a workgroup's whole K range in flight; otherwise 3-4 stages
+  // let two workgroups share a CU
+  g.nst = M <= 64 ? 8 : (g.mt >= 4 ? 3 : 4);
+  const int bm = 32 * g.mt;
+  g.m_tiles = (M + bm - 1) / bm;
+  const int64_t tiles = (int64_t)g.m_tiles * g.n_tiles;
+  // split K only as far as needed for one workgroup per CU, keeping >= 4 k steps per split
+  int s = 1;
+  if (tiles < kI8MaxSplitTiles) s = (int)std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, g.ksteps / 4));
+  g.splits = std::max(1, std::min(s, kI8MaxSplits));
+  g.m_pad = g.m_tiles * bm;
+  g.n_pad = g.n_tiles * kI8BN;
+  g.workspace_bytes = g.splits > 1 ? (size_t)g.splits * g.m_pad * g.n_pad * sizeof(float) : 0;
+  g.lds_bytes = (size_t)g.nst * (bm * kI8BK * 2 + kI8BN * kI8BK);
+  return g;
+}
+
+template <int DTYPE, int MT, int NST>
+static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, hipStream_t stream) {
+  using C = I8Cfg<MT, NST>;
+  if (lds != (size_t)C::NST * C::STAGE) return hipErrorInvalidValue;  // geometry and kernel disagree
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, C::NST * C::STAGE);
+  });
+  if (attr != hipSuccess) return attr;
+  const int nwg = p.n_tiles * p.m_tiles * p.splits;
+  hipLaunchKernelGGL((int8_gemm_kernel<DTYPE, MT, NST>), dim3(nwg), dim3(256), lds, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  const int64_t slots = (int64_t)p.n_tiles * p.m_tiles * 4 * MT * 4 * 64;
+  hipLaunchKernelGGL((int8_gemm_reduce_kernel<DTYPE, MT>), dim3((unsigned)((slots + 255) / 256)), dim3(256), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+template <int DTYPE>
+static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_t stream) {
+  if (g.mt == 1 && g.nst == 8) return launch_i8_t<DTYPE, 1, 8>(p, g.lds_bytes, stream);
+  if (g.mt == 2 && g.nst == 8) return launch_i8_t<DTYPE, 2, 8>(p, g.lds_bytes, stream);
+  if (g.mt == 2 && g.nst == 4) return launch_i8_t<DTYPE, 2, 4>(p, g.lds_bytes, stream);
+  if (g.mt == 4 && g.nst == 3) return launch_i8_t<DTYPE, 4, 3>(p, g.lds_bytes, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_int8_gemm(const I8GemmParams& p, const I8Geom& g, int dtype, hipStream_t stream) {
+  return dtype == 0 ? launch_i8_d<0>(p, g, stream) : launch_i8_d<1>(p, g, stream);
+}
+
+}  // namespace cie

@@ -135,7 +135,32 @@ struct RopeParams {
   FastDiv ldiv, hdiv;
 };
 
+// INT8-weight GEMM: y (M, N) = (x (M, K) . w (N, K)^T) * scales[n] (+ bias[n]).
+struct I8GemmParams {
+  const uint16_t* x;      // fp16 / bf16, row stride xs elements, unit column stride
+  const int8_t* w;        // row stride wsr bytes
+  const void* scales;     // (N,) fp16 / bf16 / fp32 (scale_dtype 0 / 1 / 2)
+  const uint16_t* bias;   // (N,) in x's dtype, or nullptr
+  uint16_t* y;            // row stride ys elements
+  float* partial;         // fp32 partial tiles when splits > 1 (lane order, see int8_gemm.hip)
+  int64_t xs, wsr, ys;
+  int M, N, K, scale_dtype;
+  int n_tiles, m_tiles, splits, ksteps, m_pad, n_pad;
+};
+
+// Launch geometry of an INT8 GEMM; a pure function of (M, N, K), so the
+// workspace query and the launch agree.
+struct I8Geom {
+  int mt;                  // 32-row activation tiles per workgroup
+  int nst;                 // LDS ring stages
+  int m_tiles, n_tiles, ksteps, splits, m_pad, n_pad;
+  size_t workspace_bytes;  // split-K partials (0 when splits == 1)
+  size_t lds_bytes;
+};
+I8Geom int8_gemm_geometry(int M, int N, int K);
+
 hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stream);
+hipError_t launch_int8_gemm(const I8GemmParams& p, const I8Geom& g, int dtype, hipStream_t stream);
 hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, int dtype, int D, hipStream_t stream);
 hipError_t launch_rope(const RopeParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, hipStream_t stream);

@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "cie_flash_fwd_rope",
     "cie_paged_fwd_rope",
     "cie_kv_append_rope",
+    "cie_int8_matmul_workspace_bytes",
+    "cie_int8_matmul",
 )
 
 
@@ -85,6 +87,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cie_kv_append_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                        _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i64p, _vp]
     lib.cie_kv_append_rope.restype = _i
+    lib.cie_int8_matmul_workspace_bytes.argtypes = [_i, _i, _i]
+    lib.cie_int8_matmul_workspace_bytes.restype = ctypes.c_size_t
+    lib.cie_int8_matmul.argtypes = [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                    _i, _i, _i, _i, _i, _vp, ctypes.c_size_t, _vp]
+    lib.cie_int8_matmul.restype = _i
 
 
 def load() -> ctypes.CDLL:

@@ -13,8 +13,9 @@
  *                   engine/cache/kv_cache.py:141-165 followed by flash_attention).
  *
  * Around them: cie_kv_append (the pool write of new tokens), cie_rope_apply
- * (rotary embedding) and the _rope variants that fuse the rotation into the
- * append and the query loads.
+ * (rotary embedding), the _rope variants that fuse the rotation into the
+ * append and the query loads, and cie_int8_matmul (the INT8-weight
+ * projections around attention).
  *
  * Conventions shared by every entry point:
  *   - Every pointer is a device pointer (e.g. torch.Tensor.data_ptr()).
@@ -234,6 +235,30 @@ int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void
                        int num_blocks, int block_size, int max_blocks_per_seq, int dtype,
                        const float* rope_cos, const float* rope_sin, int rope_rows,
                        void* k_out, const int64_t* k_out_stride, void* stream);
+
+/*
+ * INT8-weight linear layer: y = (x . w_int8^T) * scales[n] (+ bias[n]).
+ *   x: (M, K) fp16 / bf16 (dtype), row stride x_row_stride elements
+ *   w_int8: (N, K) int8, row stride w_row_stride bytes (multiple of 16)
+ *   scales: (N,) per output channel, fp16 / bf16 / fp32 (scale_dtype 0 / 1 / 2)
+ *   bias: (N,) in x's dtype, or NULL
+ *   y: (M, N) in x's dtype, row stride y_row_stride elements (8-byte aligned)
+ * K must be a multiple of 64. The products x * w are exact and summed in
+ * fp32; the sum is multiplied by the scale once and rounded to x's dtype,
+ * then the bias is added in x's dtype (rounded again), as the reference does.
+ * workspace: cie_int8_matmul_workspace_bytes(M, N, K) bytes, 16-byte
+ * aligned (0 bytes -- NULL allowed -- when the launch does not split K);
+ * any contents, not shared by concurrent calls. One kernel is launched on
+ * the stream, or two when K is split (the second sums the split partials).
+ * Reference: kernels/int8_matmul.py:65-110 (wrapper; bias :107-109) and
+ * :16-62 (kernel), called by Int8Linear.forward
+ * (engine/quant/int8_linear.py:37-41).
+ */
+size_t cie_int8_matmul_workspace_bytes(int M, int N, int K);
+int cie_int8_matmul(const void* x, const int8_t* w_int8, const void* scales, const void* bias, void* y,
+                    int64_t x_row_stride, int64_t w_row_stride, int64_t y_row_stride,
+                    int M, int N, int K, int dtype, int scale_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

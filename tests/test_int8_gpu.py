@@ -1,0 +1,121 @@
+"""GPU parity of the INT8-weight GEMM (engine.quant.int8_matmul ->
+cie_int8_matmul) against the oracle's restatement of the reference
+(oracle/int8_ref.py <- kernels/int8_matmul.py, kernels/ref/int8_matmul_ref.py).
+
+* the reference's own test case (tests/kernels/test_triton_kernels.py:25-41:
+  M=64, N=128, K=64, fp16, seed 0) at its tolerance, 1e-3;
+* bit-exactness at full sizes where the arithmetic is exact: integer
+  activations in [-4, 4] and power-of-two scales make every fp32 sum exact,
+  so any summation order gives the same result and the output must equal
+  the oracle's bit for bit -- at the reference's benchmark shapes
+  (64 / 512 x 4096 x 4096, benchmarks/bench_int8_matmul.py:14) and ragged
+  ones, split-K and not, with and without bias;
+* random activations against the oracle within the output rounding
+  (|y - ref| <= atol + rtol |ref|: fp16 1e-3 + 2e-3 |ref|, bf16 1e-2 + 1.6e-2 |ref|);
+* Int8Linear against the float layer it quantizes
+  (tests/quant/test_int8_linear.py:9-21: relative error < 5 %)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from engine.quant import Int8Linear, int8_matmul, int8_matmul_workspace_bytes, quantize_linear
+from oracle import int8_matmul_kernel_order_ref, int8_matmul_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float16: (1e-3, 2e-3), torch.bfloat16: (1e-2, 1.6e-2)}
+
+
+def test_reference_test_case():
+    torch.manual_seed(0)
+    M, N, K = 64, 128, 64
+    w_fp = torch.randn(N, K)
+    scales = (w_fp.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+    w_int8 = (w_fp / scales.unsqueeze(-1)).round().clamp(-128, 127).to(torch.int8)
+    x = torch.randn(M, K, dtype=torch.float16, device=DEV)
+    y = int8_matmul(x, w_int8.to(DEV), scales.to(DEV).to(torch.float16))
+    ref = int8_matmul_ref(x.cpu(), w_int8, scales.to(torch.float16))
+    assert (y.cpu() - ref).abs().max() < 1e-3
+
+
+def _exact_case(M, N, K, dtype, seed, bias):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randint(-4, 5, (M, K), generator=g).to(dtype)
+    w = torch.randint(-128, 128, (N, K), generator=g).to(torch.int8)
+    s = (2.0 ** -torch.randint(6, 10, (N,), generator=g).float()).to(torch.float16)
+    b = (torch.randn(N, generator=g) * 4).to(dtype) if bias else None
+    return x, w, s, b
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (512, 4096, 4096), (1, 4096, 4096), (33, 300, 640),
+                                   (100, 127, 64), (2048, 4096, 256), (515, 1000, 1024)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
+    for bias in (False, True):
+        x, w, s, b = _exact_case(M, N, K, dtype, seed=M + N + K, bias=bias)
+        y = int8_matmul(x.to(DEV), w.to(DEV), s.to(DEV), bias=None if b is None else b.to(DEV))
+        want = int8_matmul_kernel_order_ref(x, w, s, b)
+        assert torch.equal(y.cpu(), want), (M, N, K, bias, (y.cpu().float() - want.float()).abs().max().item())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(7, 256, 512), (64, 1024, 2048), (300, 384, 4096)])
+def test_random_activations_within_rounding(M, N, K, dtype):
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w_fp = torch.randn(N, K, generator=g) * 0.02
+    s = (w_fp.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+    w = (w_fp / s[:, None]).round().clamp(-128, 127).to(torch.int8)
+    s = s.to(torch.float16)
+    y = int8_matmul(x.to(DEV), w.to(DEV), s.to(DEV)).cpu().float()
+    ref = int8_matmul_ref(x, w, s).float()
+    atol, rtol = TOL[dtype]
+    assert ((y - ref).abs() <= atol + rtol * ref.abs()).all(), (y - ref).abs().max().item()
+
+
+def test_layouts_scale_dtypes_and_shapes():
+    g = torch.Generator().manual_seed(9)
+    B, L, K, N = 2, 5, 256, 192
+    x = torch.randint(-3, 4, (B, L, K), generator=g).half()
+    w = torch.randint(-128, 128, (N, K), generator=g).to(torch.int8)
+    s = 2.0 ** -torch.randint(5, 8, (N,), generator=g).float()
+    want = int8_matmul_kernel_order_ref(x.reshape(-1, K), w, s.half()).reshape(B, L, N)
+    for sd in (torch.float16, torch.bfloat16, torch.float32):  # powers of two: exact in each
+        y = int8_matmul(x.to(DEV), w.to(DEV), s.to(sd).to(DEV))
+        assert y.shape == (B, L, N) and torch.equal(y.cpu(), want)
+    # strided activations (a column slice of a wider buffer) and a strided weight view
+    wide = torch.zeros(B * L, K + 64).half()
+    wide[:, 32:32 + K] = x.reshape(-1, K)
+    wbig = torch.zeros(N, K + 128, dtype=torch.int8)
+    wbig[:, :K] = w
+    y = int8_matmul(wide.to(DEV)[:, 32:32 + K], wbig.to(DEV)[:, :K], s.half().to(DEV))
+    assert torch.equal(y.cpu(), want.reshape(-1, N))
+    assert int8_matmul_workspace_bytes(1, N, 4096) > 0
+
+
+def test_int8_linear_close_to_float_layer():
+    # tests/quant/test_int8_linear.py:9-21
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(64, 32, bias=True).to(device=DEV, dtype=torch.float16)
+    qlin = quantize_linear(lin).to(DEV)
+    assert isinstance(qlin, Int8Linear)
+    x = torch.randn(4, 64, device=DEV, dtype=torch.float16)
+    y_fp = lin(x)
+    y_q = qlin(x)
+    assert y_q.shape == y_fp.shape
+    assert (y_q - y_fp).abs().max().item() / y_fp.abs().max().item() < 0.05
+    # and it is the oracle's result for the quantized weights
+    ref = int8_matmul_kernel_order_ref(x.cpu(), qlin.weight_int8.cpu(), qlin.scales.cpu(), qlin.bias.detach().cpu())
+    atol, rtol = TOL[torch.float16]
+    assert ((y_q.cpu().float() - ref.float()).abs() <= atol + rtol * ref.float().abs()).all()
+
+
+def test_repeated_calls_are_deterministic():
+    x, w, s, _ = _exact_case(64, 2048, 4096, torch.float16, seed=1, bias=False)
+    xr = torch.randn(64, 4096).half().to(DEV)
+    wd, sd = w.to(DEV), s.to(DEV)
+    a = int8_matmul(xr, wd, sd)
+    for _ in range(3):
+        assert torch.equal(int8_matmul(xr, wd, sd), a)
