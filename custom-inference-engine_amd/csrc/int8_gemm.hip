@@ -235,17 +235,26 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
     wait_steps_ahead<C::PER, C::NST - 1>(min(C::NST - 1, T - 1 - t));  // steps issued after step t
     __syncthreads();  // step t is in LDS for every wave
     const uint8_t* st = smem + (t % C::NST) * C::STAGE;
+    // every fragment of the step is read first, so the LDS latency is paid
+    // once per step rather than in front of each MFMA
+    u32x4 wq[2], xb[MT][2][2];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) wq[g2] = *reinterpret_cast<const u32x4*>(st + woff[g2]);
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) xb[mt][g2][g] = *reinterpret_cast<const u32x4*>(st + xoff[mt][g2][g]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g2 = 0; g2 < 2; ++g2) {
-      const u32x4 q = *reinterpret_cast<const u32x4*>(st + woff[g2]);
       u32x4 a0, a1;
-      dequant16<DTYPE>(q, a0, a1);
+      dequant16<DTYPE>(wq[g2], a0, a1);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const u32x4 b0 = *reinterpret_cast<const u32x4*>(st + xoff[mt][g2][0]);
-        const u32x4 b1 = *reinterpret_cast<const u32x4*>(st + xoff[mt][g2][1]);
-        acc[mt] = E::mfma(a0, b0, acc[mt]);
-        acc[mt] = E::mfma(a1, b1, acc[mt]);
+        acc[mt] = E::mfma(a0, xb[mt][g2][0], acc[mt]);
+        acc[mt] = E::mfma(a1, xb[mt][g2][1], acc[mt]);
       }
     }
     __syncthreads();  // every wave is done with the slot before it is refilled
