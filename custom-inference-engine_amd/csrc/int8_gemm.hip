@@ -326,10 +326,133 @@ __global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParam
   store4<DTYPE>(p, m, n, finish4<DTYPE>(a, p, n));
 }
 
+// Decode-sized layers (M <= 32): weight streaming in one launch. A
+// workgroup owns kGvRows = 16 weight rows and its 4 waves split K into
+// quarters. A wave copies its slab in passes of up to 1 KiB per row with
+// one direct-to-LDS load per row (1 KiB contiguous per instruction: the
+// full-row-run pattern that streams at copy speed; 32-byte runs across 32
+// rows per instruction were 1.5x slower), chunks XOR-swizzled by row so the
+// MFMA-layout reads are conflict free. The weight rows fill rows 0-15 of the
+// 32-row A operand (rows 16-31 repeat them and are discarded). The
+// activation fragments come from L2 in batches of 8 k groups, one batch
+// ahead (the first two before the wait on the weight copies), loaded only
+// by lanes of rows < M. A batch's weight fragments are read from LDS together
+// before its MFMAs, which rotate over four accumulators (four independent
+// chains, summed in a fixed order); the 4 waves' partial tiles are summed
+// through LDS in wave order (deterministic), then scaled, rounded, stored.
+// Same k permutation as the tiled kernel.
+constexpr int kGvWaves = 4;
+constexpr int kGvRows = 16;
+constexpr int kGvPass = 32;    // k groups (32 k, 32 bytes of a row) per pass: 1 KiB per row
+constexpr int kGvBatch = 8;    // activation groups per batch
+constexpr int kGvSlab = kGvRows * kGvPass * 32;  // LDS bytes per wave
+
+template <int DTYPE>
+__global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
+  using E = Elt<DTYPE>;
+  __shared__ __attribute__((aligned(16))) uint8_t wl[kGvWaves * kGvSlab];
+  __shared__ f32x4_t red[kGvWaves][2][64];
+  const int n0 = blockIdx.x * kGvRows;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r32 = lane & 31, hk = lane >> 5;
+  const int G = p.K / 32;
+  const int g0 = w * G / kGvWaves, g1 = (w + 1) * G / kGvWaves;
+  const uint32_t slab = lds_addr_of(wl) + (uint32_t)(w * kGvSlab);
+  const uint8_t* slab_p = wl + w * kGvSlab;
+  const int frow = r32 & (kGvRows - 1);  // A-operand row -> weight row of the tile
+  const uint16_t* xrow = p.x + (int64_t)min(r32, p.M - 1) * p.xs + 16 * hk;
+  const bool xlive = r32 < p.M;
+  f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};  // four independent MFMA chains
+  auto load_x = [&](u32x4 (&xq)[kGvBatch][2], int gfirst, int gend) {
+#pragma unroll
+    for (int c = 0; c < kGvBatch; ++c) {
+      const bool ok = xlive && gfirst + c < gend;
+      xq[c][0] = load16(xrow + 32 * (gfirst + c), ok);
+      xq[c][1] = load16(xrow + 32 * (gfirst + c) + 8, ok);
+    }
+  };
+  for (int gp = g0; gp < g1; gp += kGvPass) {
+    const int np = min(kGvPass, g1 - gp);  // groups of this pass
+    const int gend = gp + np;
+    // the first two activation batches, then the weight copies; one wait covers them all
+    u32x4 xa[kGvBatch][2], xb[kGvBatch][2];
+    load_x(xa, gp, gend);
+    load_x(xb, gp + kGvBatch, gend);
+#pragma unroll
+    for (int rr = 0; rr < kGvRows; ++rr) {
+      // lane l fills slot l of the row: chunk l ^ rr (chunks past the pass repeat chunk 0, never read)
+      const int chunk = lane ^ rr;
+      const int ch = chunk < 2 * np ? chunk : 0;
+      const int64_t row = min(n0 + rr, p.N - 1);
+      dma16_at(reinterpret_cast<const uint8_t*>(p.w) + row * p.wsr + 32 * gp + 16 * ch, slab + rr * 1024);
+    }
+    vm_wait<0>();  // this wave's slab and activation batches 0-1 are in place (the slab is private to the wave)
+    for (int sb = 0; sb * kGvBatch < np; ++sb) {
+      const int cb = sb * kGvBatch;
+      // the batch's weight fragments first (LDS latency paid once), then dequant + MFMA
+      u32x4 wq[kGvBatch];
+#pragma unroll
+      for (int c = 0; c < kGvBatch; ++c) {
+        const int chunk = min(2 * (cb + c) + hk, 2 * kGvPass - 1);
+        wq[c] = *reinterpret_cast<const u32x4*>(slab_p + frow * 1024 + 16 * (chunk ^ frow));
+      }
+#pragma unroll
+      for (int c = 0; c < kGvBatch; ++c) {
+        if (cb + c < np) {
+          u32x4 a0, a1;
+          dequant16<DTYPE>(wq[c], a0, a1);
+          acc[(2 * c) & 3] = E::mfma(a0, xa[c][0], acc[(2 * c) & 3]);
+          acc[(2 * c + 1) & 3] = E::mfma(a1, xa[c][1], acc[(2 * c + 1) & 3]);
+        }
+      }
+      // rotate the activation batches: b -> a, next -> b
+#pragma unroll
+      for (int c = 0; c < kGvBatch; ++c) {
+        xa[c][0] = xb[c][0];
+        xa[c][1] = xb[c][1];
+      }
+      if (cb + 2 * kGvBatch < np) load_x(xb, gp + cb + 2 * kGvBatch, gend);
+    }
+  }
+  // rows 0-15 of the tile: C elements (q = 0, 1) of every lane, chains summed in a fixed order
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    f32x4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (acc[0][4 * q + e] + acc[1][4 * q + e]) + (acc[2][4 * q + e] + acc[3][4 * q + e]);
+    red[w][q][lane] = v;
+  }
+  __syncthreads();
+  if (w < 2) {  // wave q finishes weight rows 8q + 4hk .. +4 for activation row r32
+    const int q = w;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int wv = 0; wv < kGvWaves; ++wv) {
+      const f32x4_t v = red[wv][q][lane];
+      a[0] += v[0];
+      a[1] += v[1];
+      a[2] += v[2];
+      a[3] += v[3];
+    }
+    const int n = n0 + 8 * q + 4 * hk;
+    store4<DTYPE>(p, r32, n, finish4<DTYPE>(a, p, n));
+  }
+}
+
 I8Geom int8_gemm_geometry(int M, int N, int K) {
   I8Geom g{};
   g.n_tiles = (N + kI8BN - 1) / kI8BN;
   g.ksteps = K / kI8BK;
+  if (M <= 32) {  // weight streaming, one launch, no workspace
+    g.gemv = 1;
+    g.mt = 1;
+    g.m_tiles = 1;
+    g.splits = 1;
+    g.m_pad = 32;
+    g.n_pad = g.n_tiles * kI8BN;
+    return g;
+  }
   // activation tile: 32 / 64 rows for small M, 128 when that still gives one
   // (n, m) tile per CU
   if (M <= 32) g.mt = 1;
@@ -376,6 +499,11 @@ static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, hipStream_t str
 
 template <int DTYPE>
 static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_t stream) {
+  if (g.gemv) {
+    hipLaunchKernelGGL(int8_gemv_kernel<DTYPE>, dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)), dim3(64 * kGvWaves),
+                       0, stream, p);
+    return hipGetLastError();
+  }
   if (g.mt == 1 && g.nst == 8) return launch_i8_t<DTYPE, 1, 8>(p, g.lds_bytes, stream);
   if (g.mt == 2 && g.nst == 8) return launch_i8_t<DTYPE, 2, 8>(p, g.lds_bytes, stream);
   if (g.mt == 2 && g.nst == 4) return launch_i8_t<DTYPE, 2, 4>(p, g.lds_bytes, stream);

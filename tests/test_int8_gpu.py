@@ -50,7 +50,8 @@ def _exact_case(M, N, K, dtype, seed, bias):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (512, 4096, 4096), (1, 4096, 4096), (33, 300, 640),
-                                   (100, 127, 64), (2048, 4096, 256), (515, 1000, 1024)])
+                                   (100, 127, 64), (2048, 4096, 256), (515, 1000, 1024), (16, 11008, 4096),
+                                   (32, 4096, 11008), (5, 96, 64), (31, 1000, 2112)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
     for bias in (False, True):
@@ -92,7 +93,8 @@ def test_layouts_scale_dtypes_and_shapes():
     wbig[:, :K] = w
     y = int8_matmul(wide.to(DEV)[:, 32:32 + K], wbig.to(DEV)[:, :K], s.half().to(DEV))
     assert torch.equal(y.cpu(), want.reshape(-1, N))
-    assert int8_matmul_workspace_bytes(1, N, 4096) > 0
+    assert int8_matmul_workspace_bytes(1, N, 4096) == 0   # weight streaming: one launch, no workspace
+    assert int8_matmul_workspace_bytes(64, N, 4096) > 0   # split K
 
 
 def test_int8_linear_close_to_float_layer():
