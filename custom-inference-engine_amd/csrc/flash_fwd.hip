@@ -23,17 +23,36 @@
 // wave's diagonal or the key tail; a workgroup stops at the last key any of
 // its rows can see (the n_end bound of kernels/flash_attention.py:75-77).
 //
-// The running max is refreshed lazily: a row keeps its reference max m until
-// a tile raises the row max by more than 2^8 (so p <= 256, exact to fp16 /
-// bf16 rounding), and the accumulator rescale is skipped for the whole wave
-// when no row needs it. The final acc / l is unchanged by the choice of m.
+// The running max is refreshed lazily and without a per-tile row max: p(t)
+// is computed against the reference max m, and only when a lane's 32
+// probabilities of the tile sum past 2^10 (so some p may not fit the 16-bit
+// P.V operand; always the case for a row that had no visible key before)
+// does the wave recompute S(t) from the still-resident K tile, take its row
+// max, raise m to it and redo the tile. Otherwise every p <= 2^10, exact to
+// fp16 / bf16 rounding. The final acc / l is unchanged by the choice of m.
 // l accumulates the probabilities as rounded for the P.V product.
+//
+// The tile loop is unrolled by a multiple of the ring depth so that every
+// LDS stage offset is an immediate of the fragment reads.
+#include <type_traits>
+#include <utility>
+
 #include "kernels.hpp"
 #include "rope.hpp"
 
 namespace cie {
 
-constexpr float kLazyRescale = 8.0f;  // log2 of the largest p tolerated before rescaling
+constexpr float kSumTrigger = 1024.0f;  // a lane's tile sum of p above this recomputes the row max
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>), in order.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 template <int D>
 struct FlashCfg {
@@ -202,49 +221,37 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   f32x16 acc[C::DT];
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f, l2 = 0.f;  // row sum = l + l2
+  float m = -INFINITY, l = 0.f;
 
   vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
   const int pro = min(C::NST - 1, n_tiles);
   for (int t = 0; t < pro; ++t) issue(t);
 
   // Software pipeline: iteration t holds S(t) in registers, computes
-  // S(t+1) = K(t+1) Q^T while turning S(t) into P(t), then O += V(t) P(t)
-  // while reducing the row max of S(t+1). Tiles t and t+1 are resident; the
-  // copies of the next NST-2 tiles are in flight.
+  // S(t+1) = K(t+1) Q^T while turning S(t) into P(t), then O += V(t) P(t).
+  // Tiles t and t+1 are resident; the copies of the next NST-2 tiles are in
+  // flight.
   f32x16 sc[C::MT];
-  float mx = -INFINITY;
   if (n_tiles > 0) {
     wait_ahead<C::NST, C::PER_TILE>(pro - 1);
     __syncthreads();
     qk(0, sc);
     mask(0, sc);
-    mx = rowmax(sc);
+    m = xhalf_max(rowmax(sc)) * c;  // the reference max starts at tile 0's row max
   }
   const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
-  // One pipeline step: sc holds S(t), S(t+1) is produced in sn. The loop
-  // below runs it twice per trip with the two score arrays swapped, so the
-  // scores are never copied between registers.
-  auto step = [&](const int t, f32x16* sc, f32x16* sn) {
+  // One pipeline step: sc holds S(t), S(t+1) is produced in sn; ST is the
+  // ring stage of tile t (t % NST). The loop below runs U steps per trip with
+  // the two score arrays swapped each step, so the scores are never copied
+  // between registers.
+  auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) {
+    constexpr int st = decltype(ST)::value, st1 = (st + 1) % C::NST;
     if (t + 1 < n_tiles) {
       wait_ahead<C::NST, C::PER_TILE>(min(C::NST - 3, n_tiles - 2 - t));
       __syncthreads();  // tile t+1 resident for all waves; stage of tile t-1 free
       if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
     }
     if (t * BN >= wave_kend) return;  // wave-uniform: every row of the wave is done
-
-    // lazy rescale against the row max of S(t)
-    const float mxs = xhalf_max(mx) * c;
-    const bool grow = mxs > m + kLazyRescale;
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-      const float m_new = grow ? mxs : m;
-      const float alpha = grow ? exp2_fast(m - m_new) : 1.f;  // 0 when m was -inf
-      l *= alpha;
-      l2 *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
-      m = m_new;
-    }
     const float neg_m = m == -INFINITY ? 0.f : -m;
 
     // (c) S(t+1) on the MFMA pipe, P(t) on the VALU, interleaved by hand:
@@ -258,8 +265,9 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // wave's P.V phase fills the gaps (measured 4-5 % faster at D=64).
     __builtin_amdgcn_s_setprio(1);
     u32x4 pb[2 * C::MT];
+    float ts0 = 0.f, ts1 = 0.f;  // this lane's sum of the tile's p (two chains)
     {
-      const uint16_t* ks = ring + ((t + 1) % C::NST) * C::STAGE;
+      const uint16_t* ks = ring + st1 * C::STAGE;
       u32x4 ka[C::NQK];
 #pragma unroll
       for (int i = 0; i < C::NQK; ++i) {
@@ -284,8 +292,8 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
             const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
             asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
             pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
-            if (ee & 2) l2 = E::sum2(pk, l2);
-            else l = E::sum2(pk, l);
+            if (ee & 2) ts1 = E::sum2(pk, ts1);
+            else ts0 = E::sum2(pk, ts0);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -293,11 +301,41 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     }
 
     __builtin_amdgcn_s_setprio(0);
+
+    // Slow path of the lazy max (rare: a row's max rose by ~2^5 or more, or
+    // its first visible key): S(t) again from the resident K tile, m raised
+    // to the row max, accumulators rescaled, the tile's p recomputed.
+    float ts = ts0 + ts1;
+    if (__builtin_amdgcn_ballot_w64(!(ts <= kSumTrigger))) {
+      qk(t, sc);
+      mask(t, sc);
+      const float mxs = xhalf_max(rowmax(sc)) * c;
+      const bool grow = mxs > m;
+      const float m_new = grow ? mxs : m;
+      const float alpha = grow ? exp2_fast(m - m_new) : 1.f;  // 0 when m was -inf
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+      m = m_new;
+      const float nm = m == -INFINITY ? 0.f : -m;
+      ts0 = 0.f;
+      ts1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16 * C::MT; e += 2) {
+        const int m2 = e / 16, ee = e % 16;
+        const uint32_t pk = E::pack2(exp2_fast(fmaf(sc[m2][ee], c, nm)), exp2_fast(fmaf(sc[m2][ee + 1], c, nm)));
+        pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
+        if (ee & 2) ts1 = E::sum2(pk, ts1);
+        else ts0 = E::sum2(pk, ts0);
+      }
+      ts = ts0 + ts1;
+    }
+    l += ts;
     mask(t + 1, sn);
 
-    // (d) O += V(t) P(t) on the MFMA pipe, row max of S(t+1) on the VALU.
+    // (d) O += V(t) P(t) on the MFMA pipe.
     {
-      const uint16_t* vs = ring + (t % C::NST) * C::STAGE + C::TILE;
+      const uint16_t* vs = ring + st * C::STAGE + C::TILE;
       u32x4 va[C::NPV];
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
@@ -317,23 +355,24 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
       for (int i = 0; i < C::NPV; ++i) {
         const int dt = i % C::DT, cc = i / C::DT;  // alternate accumulators
         acc[dt] = E::mfma(va[dt * 2 * C::MT + cc], pb[cc], acc[dt]);
-        if (i == C::NPV / 2) {
-          __builtin_amdgcn_sched_barrier(0);
-          mx = rowmax(sn);
-          __builtin_amdgcn_sched_barrier(0);
-        }
       }
     }
   };
   f32x16 sb[C::MT];
-  for (int t = 0; t < n_tiles; t += 2) {
-    step(t, sc, sb);
-    if (t + 1 < n_tiles) step(t + 1, sb, sc);
+  constexpr int U = C::NST % 2 == 0 ? C::NST : 2 * C::NST;  // steps per trip: stage and score buffer both repeat
+  for (int t = 0; t < n_tiles; t += U) {
+    static_for<U>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (t + i < n_tiles) {
+        if constexpr (i % 2 == 0) step(std::integral_constant<int, i % C::NST>{}, t + i, sc, sb);
+        else step(std::integral_constant<int, i % C::NST>{}, t + i, sb, sc);
+      }
+    });
   }
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
   // reference's softmax over an all -inf row; Lk == 0 gives zeros.
-  const float l_tot = xhalf_sum(l + l2);
+  const float l_tot = xhalf_sum(l);
   const float inv = p.Lk == 0 ? 0.f : 1.f / l_tot;
   if (qi < p.Lq) {
     uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)qi * p.os2;

@@ -119,6 +119,37 @@ def test_gqa_equals_expanded_mha_bitwise():
     assert torch.equal(gqa, mha)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("pattern", ["rising", "spikes", "falling"])
+def test_row_max_changes_across_tiles(D, dtype, pattern):
+    """Scores whose row max moves by many log2 units from tile to tile: the
+    kernel keeps a reference max per row and recomputes it only when a tile's
+    probabilities outgrow it (rising scores do so on every tile; spikes on a
+    few; falling never), so each pattern takes a different path."""
+    g = torch.Generator().manual_seed(D + len(pattern))
+    B, H, Hk, L = 1, 4, 2, 640
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    q = (torch.randn(B, H, L, D, generator=g) * 0.3 + 3.0 * u).to(dtype)
+    k = torch.randn(B, Hk, L, D, generator=g) * 0.3
+    pos = torch.arange(L, dtype=torch.float32)
+    c = math.log2(math.e) / math.sqrt(D)  # log2 units of score per unit of q.k
+    if pattern == "rising":      # +20 log2 units of score per 64 keys
+        k += (pos / 64.0 * 20.0 / (3.0 * c))[None, None, :, None] * u
+    elif pattern == "spikes":    # a few keys, each 5-20 log2 units above the ones before
+        for j, h in ((5, 10.0), (150, 20.0), (151, 20.0), (400, 30.0), (639, 40.0)):
+            k[:, :, j] += h * u
+    else:                        # the first keys dominate
+        k += ((L - pos) / L * 4.0)[None, None, :, None] * u
+    k = k.to(dtype)
+    v = (torch.randn(B, Hk, L, D, generator=g) * 0.5).to(dtype)
+    for causal in (True, False):
+        out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
+        ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=causal)
+        assert_close(out, ref, TOL[dtype], f"{pattern} D={D} {dtype} causal={causal}")
+
+
 def test_deterministic():
     q, k, v = _inputs(1, 8, 2, 257, 257, 128, torch.bfloat16, seed=10)
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
