@@ -42,6 +42,10 @@
 
 namespace cie {
 
+// Every lambda of the kernel is inlined: the score arrays they take by
+// pointer must stay in registers.
+#define CIE_INLINE __attribute__((always_inline))
+
 constexpr float kSumTrigger = 1024.0f;  // a lane's tile sum of p above this recomputes the row max
 
 // f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>), in order.
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     voff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.vs2 + lchk[j])) : 0u;
   }
   const uint32_t ring_lds = lds_addr_of(ring);
-  auto issue = [&](int t) {
+  auto issue = [&](int t) CIE_INLINE {
     const int n0 = t * BN;
     const uint32_t st = ring_lds + 2u * (uint32_t)((t % C::NST) * C::STAGE + wave * C::NW * 512);
     if (off32 && n0 + BN <= p.Lk) {
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 
   // S^T of tile t from its ring stage (rows past the tile data are finite
   // copies of the last key or stale LDS; the caller masks or discards them).
-  auto qk = [&](int t, f32x16* s) {
+  auto qk = [&](int t, f32x16* s) CIE_INLINE {
     const uint16_t* ks = ring + (t % C::NST) * C::STAGE;
 #pragma unroll
     for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
@@ -199,7 +203,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   };
   // Bottom-right causal / key-tail mask of tile t (only tiles that cross the
   // smallest visible limit of the wave need it).
-  auto mask = [&](int t, f32x16* s) {
+  auto mask = [&](int t, f32x16* s) CIE_INLINE {
     const int n0 = t * BN;
     if (n0 + BN - 1 > wave_lim0) {
 #pragma unroll
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
         }
     }
   };
-  auto rowmax = [&](const f32x16* s) {
+  auto rowmax = [&](const f32x16* s) CIE_INLINE {
     float mx = max16(s[0]);
 #pragma unroll
     for (int mt2 = 1; mt2 < C::MT; ++mt2) mx = maxf(mx, max16(s[mt2]));
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   // ring stage of tile t (t % NST). The loop below runs U steps per trip with
   // the two score arrays swapped each step, so the scores are never copied
   // between registers.
-  auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) {
+  auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
     constexpr int st = decltype(ST)::value, st1 = (st + 1) % C::NST;
     if (t + 1 < n_tiles) {
       wait_ahead<C::NST, C::PER_TILE>(min(C::NST - 3, n_tiles - 2 - t));
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   f32x16 sb[C::MT];
   constexpr int U = C::NST % 2 == 0 ? C::NST : 2 * C::NST;  // steps per trip: stage and score buffer both repeat
   for (int t = 0; t < n_tiles; t += U) {
-    static_for<U>([&](auto I) {
+    static_for<U>([&](auto I) CIE_INLINE {
       constexpr int i = decltype(I)::value;
       if (t + i < n_tiles) {
         if constexpr (i % 2 == 0) step(std::integral_constant<int, i % C::NST>{}, t + i, sc, sb);
