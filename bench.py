@@ -561,7 +561,7 @@ def main():
                                             "dtype": "fp16", "timing": "graph replay"}
         del rl
         extra["prefill_section_b4_s2048_rope"] = prefill_section_times(dev)
-        for M in (1, 16, 64, 512):
+        for M in (1, 4, 16, 64, 512):
             il = Int8Launch(M, dev)
             ms = graph_time_ms(il, n_inner=il.copies)
             gbs = il.bytes / (ms / 1e3) / 1e9

@@ -47,6 +47,10 @@ template <> struct Elt<0> {
   static __device__ __forceinline__ float sum2(uint32_t pk, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk), f16x2{(_Float16)1.f, (_Float16)1.f}, acc, false);
   }
+  // acc + a.lo * b.lo + a.hi * b.hi, fp32 accumulation of exact products.
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+  }
 };
 
 template <> struct Elt<1> {
@@ -60,6 +64,9 @@ template <> struct Elt<1> {
   static __device__ __forceinline__ float sum2(uint32_t pk, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), bf16x2{(__bf16)1.f, (__bf16)1.f}, acc,
                                            false);
+  }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
   }
 };
 

@@ -35,10 +35,24 @@
 // atomic and coherent reloads in series; on MI355X that chain cost more than
 // the second launch.)
 #include <mutex>
+#include <type_traits>
+#include <utility>
 
 #include "kernels.hpp"
 
 namespace cie {
+
+#define CIE_GV_INLINE __attribute__((always_inline))
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>), in order.
+template <typename F, int... I>
+__device__ __forceinline__ void gv_static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void gv_static_for(F&& f) {
+  gv_static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -440,12 +454,115 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
   }
 }
 
+// Decode at M <= 4: VALU dot products. The MFMA operand of the kernel above
+// spans 32 activation rows, so at M = 1 it computes 32x the products it
+// keeps and still loads each wave's whole K share before its first MFMA.
+// Here a single-wave workgroup streams kDotRows weight rows in 1 KiB chunks
+// (lane l covers k = 1024 c + 16 l .. +16 of chunk c: one 16-byte load per
+// row and chunk, the contiguous-run pattern), kDotDepth chunks ahead in a
+// register ring, with the activation fragments of the same k (read from L2)
+// in the same ring. Each chunk is dequantized exactly as in the MFMA path and
+// multiplied into fp32 accumulators with v_dot2 (products exact in fp32); a
+// fixed xor butterfly over the 64 lanes then sums every (row, activation row)
+// and lane r * MC + m finishes output (m, n0 + r). Two rows per wave and two
+// chunks ahead measured fastest at M = 1-4 among 1-16 rows and 2-8 chunks
+// (more waves in flight beat deeper per-wave rings).
+constexpr int kDotRows = 2;
+constexpr int kDotDepth = 2;
+constexpr int kDotMaxM = 4;  // from M = 5 the MFMA kernel is as fast
+
+template <int DTYPE, int MC>
+__global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p) {
+  using E = Elt<DTYPE>;
+  constexpr int PERC = kDotRows + 2 * MC;  // loads per chunk
+  const int lane = threadIdx.x;
+  const int n0 = blockIdx.x * kDotRows;
+  const int nch = (p.K + 1023) >> 10;
+  const bool tail = (p.K & 1023) != 0;
+  // rows past N / M are clamped to the last one (loaded, never stored)
+  const int8_t* wrow[kDotRows];
+#pragma unroll
+  for (int r = 0; r < kDotRows; ++r) wrow[r] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.wsr;
+  const uint16_t* xrow[MC];
+#pragma unroll
+  for (int m = 0; m < MC; ++m) xrow[m] = p.x + (int64_t)min(m, p.M - 1) * p.xs;
+
+  u32x4 wq[kDotDepth][kDotRows], xq[kDotDepth][MC][2];
+  // chunk c into ring slot s; lanes past K (last chunk) read its last 16 k, zeroed before use
+  auto issue = [&](auto S, int c) CIE_GV_INLINE {
+    constexpr int s = decltype(S)::value;
+    const int k = min(1024 * c + 16 * lane, p.K - 16);
+#pragma unroll
+    for (int r = 0; r < kDotRows; ++r) wq[s][r] = *reinterpret_cast<const u32x4*>(wrow[r] + k);
+#pragma unroll
+    for (int m = 0; m < MC; ++m) {
+      xq[s][m][0] = load16_clamped(xrow[m] + k);
+      xq[s][m][1] = load16_clamped(xrow[m] + k + 8);
+    }
+  };
+  float acc[kDotRows][MC];
+#pragma unroll
+  for (int r = 0; r < kDotRows; ++r)
+#pragma unroll
+    for (int m = 0; m < MC; ++m) acc[r][m] = 0.f;
+
+  gv_static_for<kDotDepth>([&](auto S) CIE_GV_INLINE {
+    if (decltype(S)::value < nch) issue(S, decltype(S)::value);
+  });
+  for (int c0 = 0; c0 < nch; c0 += kDotDepth) {
+    gv_static_for<kDotDepth>([&](auto S) CIE_GV_INLINE {
+      constexpr int s = decltype(S)::value;
+      const int c = c0 + s;
+      if (c < nch) {  // wave-uniform
+        wait_steps_ahead<PERC, kDotDepth - 1>(min(kDotDepth - 1, nch - 1 - c));
+        const bool kin = !(tail && c == nch - 1) || 1024 * c + 16 * lane < p.K;
+#pragma unroll
+        for (int r = 0; r < kDotRows; ++r) {
+          u32x4 a0, a1;
+          dequant16<DTYPE>(zero_unless(wq[s][r], kin), a0, a1);
+#pragma unroll
+          for (int m = 0; m < MC; ++m) {
+            float t = acc[r][m];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t = E::dot2(a0[i], xq[s][m][0][i], t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t = E::dot2(a1[i], xq[s][m][1][i], t);
+            acc[r][m] = t;
+          }
+        }
+        if (c + kDotDepth < nch) issue(S, c + kDotDepth);
+      }
+    });
+  }
+
+  float out = 0.f;
+#pragma unroll
+  for (int r = 0; r < kDotRows; ++r)
+#pragma unroll
+    for (int m = 0; m < MC; ++m) {
+      float v = acc[r][m];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+      if (lane == r * MC + m) out = v;
+    }
+  const int r = lane / MC, m = lane - (lane / MC) * MC;
+  if (lane < kDotRows * MC && m < p.M && n0 + r < p.N) {
+    const int n = n0 + r;
+    float t = out * load_scale(p.scales, n, p.scale_dtype);
+    if (p.bias) {  // the reference adds the bias to the rounded product, in the output dtype
+      const uint32_t rr = Elt<DTYPE>::pack2(t, 0.f);
+      t = elt_to_f32<DTYPE>((uint16_t)rr) + elt_to_f32<DTYPE>(p.bias[n]);
+    }
+    p.y[(int64_t)m * p.ys + n] = (uint16_t)Elt<DTYPE>::pack2(t, 0.f);
+  }
+}
+
 I8Geom int8_gemm_geometry(int M, int N, int K) {
   I8Geom g{};
   g.n_tiles = (N + kI8BN - 1) / kI8BN;
   g.ksteps = K / kI8BK;
-  if (M <= 32) {  // weight streaming, one launch, no workspace
-    g.gemv = 1;
+  if (M <= 32) {  // weight streaming, one launch, no workspace (2: VALU dot products)
+    g.gemv = M <= kDotMaxM ? 2 : 1;
     g.mt = 1;
     g.m_tiles = 1;
     g.splits = 1;
@@ -499,6 +616,13 @@ static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, hipStream_t str
 
 template <int DTYPE>
 static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_t stream) {
+  if (g.gemv == 2) {
+    const dim3 grid((unsigned)((p.N + kDotRows - 1) / kDotRows));
+    if (p.M <= 1) hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 1>), grid, dim3(64), 0, stream, p);
+    else if (p.M <= 2) hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 2>), grid, dim3(64), 0, stream, p);
+    else hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 4>), grid, dim3(64), 0, stream, p);
+    return hipGetLastError();
+  }
   if (g.gemv) {
     hipLaunchKernelGGL(int8_gemv_kernel<DTYPE>, dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)), dim3(64 * kGvWaves),
                        0, stream, p);

@@ -51,7 +51,9 @@ def _exact_case(M, N, K, dtype, seed, bias):
 
 @pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (512, 4096, 4096), (1, 4096, 4096), (33, 300, 640),
                                    (100, 127, 64), (2048, 4096, 256), (515, 1000, 1024), (16, 11008, 4096),
-                                   (32, 4096, 11008), (5, 96, 64), (31, 1000, 2112)])
+                                   (32, 4096, 11008), (5, 96, 64), (31, 1000, 2112),
+                                   # the dot-product kernel (M <= 4): ragged N, K tails within a 1 KiB chunk
+                                   (2, 300, 640), (3, 1001, 2112), (4, 130, 1088), (1, 7, 64), (1, 11008, 4096)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
     for bias in (False, True):
@@ -62,7 +64,7 @@ def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,N,K", [(7, 256, 512), (64, 1024, 2048), (300, 384, 4096)])
+@pytest.mark.parametrize("M,N,K", [(1, 512, 4096), (3, 256, 1600), (7, 256, 512), (64, 1024, 2048), (300, 384, 4096)])
 def test_random_activations_within_rounding(M, N, K, dtype):
     g = torch.Generator().manual_seed(M * 7 + K)
     x = torch.randn(M, K, generator=g).to(dtype)
