@@ -147,14 +147,15 @@ class PagedLaunch:
         self.head = (self.q.data_ptr(),)
         self.tail = (self.bt.data_ptr(), self.lens.data_ptr(), self.o.data_ptr(), self.ws.data_ptr(), ws,
                      *self._keep, B, Hq, Hk, Lq, D, nb, bs, mb, mc, ctypes.c_float(1.0 / math.sqrt(D)), 1,
-                     _lib.DTYPE_CODES[self.q.dtype], _lib.stream_handle(self.q.device))
+                     _lib.DTYPE_CODES[self.q.dtype])
+        self.dev = dev
         self.ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in self.pools]
         self.bytes = case.bytes
         self.flops = case.flops
 
     def __call__(self, i=0):
         kp, vp = self.ptrs[i % self.copies]
-        rc = self.lib.cie_paged_fwd(self.q.data_ptr(), kp, vp, *self.tail)
+        rc = self.lib.cie_paged_fwd(self.q.data_ptr(), kp, vp, *self.tail, _stream(self.dev))
         if rc:
             from engine import _lib
             _lib.check(rc)
