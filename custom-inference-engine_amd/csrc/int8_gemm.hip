@@ -25,8 +25,12 @@
 // x operand takes x[m_r][16h .. 16h+16) split the same way, so MFMA 0
 // contracts k in {0..7, 16..23} and MFMA 1 k in {8..15, 24..31}.
 //
-// Split K. When the (n, m) tiles alone cannot occupy the GPU (small M:
-// decode), the K steps are cut into `splits` contiguous ranges; each
+// Kernels by M: up to 2 a VALU dot-product kernel, up to 64 a weight-streaming
+// MFMA kernel (both one launch, no workspace; below), above that the tiled
+// kernel described here.
+//
+// Split K. When the (n, m) tiles alone cannot occupy the GPU, the K steps
+// are cut into `splits` contiguous ranges; each
 // workgroup writes its fp32 partial tile to the workspace in lane order
 // (16 contiguous bytes per lane, 1 KiB per wave instruction) and a second
 // kernel sums the partials of every output in split order (deterministic),
@@ -340,121 +344,199 @@ __global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParam
   store4<DTYPE>(p, m, n, finish4<DTYPE>(a, p, n));
 }
 
-// Decode-sized layers (M <= 32): weight streaming in one launch. A
+// Decode-sized layers (2 < M <= 64): weight streaming in one launch. A
 // workgroup owns kGvRows = 16 weight rows and its 4 waves split K into
-// quarters. A wave copies its slab in passes of up to 1 KiB per row with
-// one direct-to-LDS load per row (1 KiB contiguous per instruction: the
-// full-row-run pattern that streams at copy speed; 32-byte runs across 32
-// rows per instruction were 1.5x slower), chunks XOR-swizzled by row so the
-// MFMA-layout reads are conflict free. The weight rows fill rows 0-15 of the
-// 32-row A operand (rows 16-31 repeat them and are discarded). The
-// activation fragments come from L2 in batches of 8 k groups, one batch
-// ahead (the first two before the wait on the weight copies), loaded only
-// by lanes of rows < M. A batch's weight fragments are read from LDS together
-// before its MFMAs, which rotate over four accumulators (four independent
-// chains, summed in a fixed order); the 4 waves' partial tiles are summed
-// through LDS in wave order (deterministic), then scaled, rounded, stored.
-// Same k permutation as the tiled kernel.
+// quarters. A wave streams its quarter in passes of PG 32-k groups: per pass
+// WI direct-to-LDS loads move the 16 weight rows (32 PG contiguous bytes of
+// each) and XI more move the staged activation rows (64 PG contiguous bytes
+// of each; rows past M repeat row M - 1), into a private ring of NS pass
+// buffers, so the copies run up to NS - 1 passes ahead of the dequant +
+// MFMA work. Staging the activations through LDS keeps the vector-memory
+// instructions per pass at WI + XI (loading the 32-column MFMA operand per
+// lane took 8 per 128 k, and those loads, not the weight bytes, bounded the
+// kernel). Chunks are XOR-swizzled by row so the fragment reads are
+// conflict-free for the weights and at most 2-way for the activations. The
+// weight rows fill rows 0-15 of the 32-row A operand (rows 16-31 repeat
+// them and are discarded); MT 32-column tiles of activations. MFMAs rotate
+// over 4 / MT accumulators per tile (independent chains, summed in a fixed
+// order); the 4 waves' partial tiles are summed through LDS in wave order
+// (deterministic), then scaled, rounded, stored. Same k permutation as the
+// tiled kernel.
 constexpr int kGvWaves = 4;
 constexpr int kGvRows = 16;
-constexpr int kGvPass = 32;    // k groups (32 k, 32 bytes of a row) per pass: 1 KiB per row
-constexpr int kGvBatch = 8;    // activation groups per batch
-constexpr int kGvSlab = kGvRows * kGvPass * 32;  // LDS bytes per wave
 
-template <int DTYPE>
+template <int XROWS, int MT>
+struct WsCfg {
+  static constexpr int PG = MT == 1 ? 4 : 2;            // 32-k groups per pass
+  static constexpr int WRB = 32 * PG;                   // bytes of a weight row per pass
+  static constexpr int WCH = WRB / 16;                  // its 16-byte chunks
+  static constexpr int WRI = 64 / WCH;                  // weight rows per copy instruction
+  static constexpr int WI = kGvRows / WRI;              // weight copies per pass
+  static constexpr int WPH = 256 / WRB;                 // rows sharing a bank phase
+  static constexpr int XRB = 64 * PG;                   // bytes of an activation row per pass
+  static constexpr int XCH = XRB / 16;
+  static constexpr int XRI = 64 / XCH;                  // activation rows per copy instruction
+  static constexpr int XI = XROWS / XRI;                // activation copies per pass
+  static constexpr int XPH = 256 / XRB;
+  static constexpr int WBYTES = kGvRows * WRB;
+  static constexpr int PASS = WBYTES + XROWS * XRB;     // LDS bytes per pass buffer
+  static constexpr int NS = XROWS >= 32 ? 3 : 4;        // pass buffers per wave
+  static constexpr int PER = WI + XI;                   // copies per pass
+  static constexpr int CH = 4 / MT;                     // accumulator chains per tile
+  static constexpr int LDS = kGvWaves * NS * PASS;
+  static_assert(XROWS >= 32 * MT || MT == 1, "staged rows cover the tiles");
+  static_assert((NS - 1) * PER < 64, "vmcnt range");
+  static_assert(WI * WRI == kGvRows && XI * XRI == XROWS, "copies split evenly");
+  // chunk swizzles: rows in one bank phase get distinct chunk positions
+  static __device__ __forceinline__ int wswz(int row) { return (row / WPH) % WCH; }
+  static __device__ __forceinline__ int xswz(int row) { return (row / XPH) % XCH; }
+};
+
+template <int DTYPE, int XROWS, int MT>
 __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
   using E = Elt<DTYPE>;
-  __shared__ __attribute__((aligned(16))) uint8_t wl[kGvWaves * kGvSlab];
-  __shared__ f32x4_t red[kGvWaves][2][64];
+  using C = WsCfg<XROWS, MT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t ws_lds[];
+  __shared__ f32x4_t red[kGvWaves][MT][2][64];
   const int n0 = blockIdx.x * kGvRows;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r32 = lane & 31, hk = lane >> 5;
   const int G = p.K / 32;
   const int g0 = w * G / kGvWaves, g1 = (w + 1) * G / kGvWaves;
-  const uint32_t slab = lds_addr_of(wl) + (uint32_t)(w * kGvSlab);
-  const uint8_t* slab_p = wl + w * kGvSlab;
+  const int NP = (g1 - g0 + C::PG - 1) / C::PG;  // passes of this wave (wave-uniform)
+  const uint32_t ring = lds_addr_of(ws_lds) + (uint32_t)(w * C::NS * C::PASS);
+  const uint8_t* ring_p = ws_lds + w * C::NS * C::PASS;
   const int frow = r32 & (kGvRows - 1);  // A-operand row -> weight row of the tile
-  const uint16_t* xrow = p.x + (int64_t)min(r32, p.M - 1) * p.xs + 16 * hk;
-  const bool xlive = r32 < p.M;
-  f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};  // four independent MFMA chains
-  auto load_x = [&](u32x4 (&xq)[kGvBatch][2], int gfirst, int gend) {
+  // weight copy i: lane -> row WRI i + lane / WCH, stored chunk lane % WCH,
+  // which holds chunk (lane % WCH) ^ wswz(row) of the row's pass bytes
+  const uint8_t* wsrc[C::WI];
+  int wcg[C::WI];  // 32-k group (within the pass) of this lane's chunk
 #pragma unroll
-    for (int c = 0; c < kGvBatch; ++c) {
-      const bool ok = xlive && gfirst + c < gend;
-      xq[c][0] = load16(xrow + 32 * (gfirst + c), ok);
-      xq[c][1] = load16(xrow + 32 * (gfirst + c) + 8, ok);
-    }
+  for (int i = 0; i < C::WI; ++i) {
+    const int rr = C::WRI * i + lane / C::WCH;
+    const int c = (lane % C::WCH) ^ C::wswz(rr);
+    wsrc[i] = reinterpret_cast<const uint8_t*>(p.w) + (int64_t)min(n0 + rr, p.N - 1) * p.wsr + 16 * (c & 1);
+    wcg[i] = c >> 1;
+  }
+  // activation copy i: lane -> row XRI i + lane / XCH, stored chunk lane % XCH,
+  // which holds chunk (lane % XCH) ^ xswz(row)
+  const uint16_t* xsrc[C::XI];
+  int xcg[C::XI];
+#pragma unroll
+  for (int i = 0; i < C::XI; ++i) {
+    const int rr = C::XRI * i + lane / C::XCH;
+    const int c = (lane % C::XCH) ^ C::xswz(rr);
+    xsrc[i] = p.x + (int64_t)min(rr, p.M - 1) * p.xs + 8 * (c & 3);
+    xcg[i] = c >> 2;
+  }
+  // pass q (< NP) into buffer q % NS; groups past the end of K are clamped
+  // to the last group (loaded, never used)
+  auto issue = [&](int q) CIE_GV_INLINE {
+    const int gq = g0 + C::PG * q;
+    const uint32_t dst = ring + (uint32_t)((q % C::NS) * C::PASS);
+#pragma unroll
+    for (int i = 0; i < C::WI; ++i) dma16_at(wsrc[i] + 32 * (int64_t)min(gq + wcg[i], G - 1), dst + 1024u * i);
+#pragma unroll
+    for (int i = 0; i < C::XI; ++i)
+      dma16_at(xsrc[i] + 32 * (int64_t)min(gq + xcg[i], G - 1), dst + (uint32_t)C::WBYTES + 1024u * i);
   };
-  for (int gp = g0; gp < g1; gp += kGvPass) {
-    const int np = min(kGvPass, g1 - gp);  // groups of this pass
-    const int gend = gp + np;
-    // the first two activation batches, then the weight copies; one wait covers them all
-    u32x4 xa[kGvBatch][2], xb[kGvBatch][2];
-    load_x(xa, gp, gend);
-    load_x(xb, gp + kGvBatch, gend);
+
+  f32x16 acc[MT][C::CH];
 #pragma unroll
-    for (int rr = 0; rr < kGvRows; ++rr) {
-      // lane l fills slot l of the row: chunk l ^ rr (chunks past the pass repeat chunk 0, never read)
-      const int chunk = lane ^ rr;
-      const int ch = chunk < 2 * np ? chunk : 0;
-      const int64_t row = min(n0 + rr, p.N - 1);
-      dma16_at(reinterpret_cast<const uint8_t*>(p.w) + row * p.wsr + 32 * gp + 16 * ch, slab + rr * 1024);
-    }
-    vm_wait<0>();  // this wave's slab and activation batches 0-1 are in place (the slab is private to the wave)
-    for (int sb = 0; sb * kGvBatch < np; ++sb) {
-      const int cb = sb * kGvBatch;
-      // the batch's weight fragments first (LDS latency paid once), then dequant + MFMA
-      u32x4 wq[kGvBatch];
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int c = 0; c < kGvBatch; ++c) {
-        const int chunk = min(2 * (cb + c) + hk, 2 * kGvPass - 1);
-        wq[c] = *reinterpret_cast<const u32x4*>(slab_p + frow * 1024 + 16 * (chunk ^ frow));
+    for (int ch = 0; ch < C::CH; ++ch) acc[mt][ch] = f32x16{};
+#pragma unroll
+  for (int q = 0; q < C::NS; ++q)
+    if (q < NP) issue(q);
+  for (int q = 0; q < NP; ++q) {
+    // copies issued after pass q's: those of passes q+1 .. min(q+NS-1, NP-1)
+    const int ahead = min(C::NS - 1, NP - 1 - q);
+    if (C::NS > 3 && ahead >= 3) vm_wait<(C::NS > 3 ? 3 : 0) * C::PER>();
+    else if (ahead == 2) vm_wait<2 * C::PER>();
+    else if (ahead == 1) vm_wait<C::PER>();
+    else vm_wait<0>();
+    const uint8_t* buf = ring_p + (q % C::NS) * C::PASS;
+    const int ng = min(C::PG, g1 - g0 - C::PG * q);  // groups of this pass
+    u32x4 wq[C::PG], xq[MT][C::PG][2];
+#pragma unroll
+    for (int gi = 0; gi < C::PG; ++gi) {
+      const int wc = 2 * gi + hk;
+      wq[gi] = *reinterpret_cast<const u32x4*>(buf + frow * C::WRB + 16 * (wc ^ C::wswz(frow)));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int xr = min(32 * mt + r32, XROWS - 1);  // B-operand column -> staged activation row
+        const uint8_t* xb = buf + C::WBYTES + xr * C::XRB;
+        const int xc = 4 * gi + 2 * hk;
+        xq[mt][gi][0] = *reinterpret_cast<const u32x4*>(xb + 16 * (xc ^ C::xswz(xr)));
+        xq[mt][gi][1] = *reinterpret_cast<const u32x4*>(xb + 16 * ((xc + 1) ^ C::xswz(xr)));
       }
+    }
 #pragma unroll
-      for (int c = 0; c < kGvBatch; ++c) {
-        if (cb + c < np) {
-          u32x4 a0, a1;
-          dequant16<DTYPE>(wq[c], a0, a1);
-          acc[(2 * c) & 3] = E::mfma(a0, xa[c][0], acc[(2 * c) & 3]);
-          acc[(2 * c + 1) & 3] = E::mfma(a1, xa[c][1], acc[(2 * c + 1) & 3]);
+    for (int gi = 0; gi < C::PG; ++gi) {
+      if (gi < ng) {
+        u32x4 a0, a1;
+        dequant16<DTYPE>(wq[gi], a0, a1);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][(2 * gi) % C::CH] = E::mfma(a0, xq[mt][gi][0], acc[mt][(2 * gi) % C::CH]);
+          acc[mt][(2 * gi + 1) % C::CH] = E::mfma(a1, xq[mt][gi][1], acc[mt][(2 * gi + 1) % C::CH]);
         }
       }
-      // rotate the activation batches: b -> a, next -> b
-#pragma unroll
-      for (int c = 0; c < kGvBatch; ++c) {
-        xa[c][0] = xb[c][0];
-        xa[c][1] = xb[c][1];
-      }
-      if (cb + 2 * kGvBatch < np) load_x(xb, gp + cb + 2 * kGvBatch, gend);
     }
+    lgkm_wait0();  // this buffer's reads are complete before it is refilled
+    if (q + C::NS < NP) issue(q + C::NS);
   }
-  // rows 0-15 of the tile: C elements (q = 0, 1) of every lane, chains summed in a fixed order
+  vm_wait<0>();  // no copy into LDS may be in flight when the workgroup ends
+  // rows 0-15 of each tile: C elements (q = 0, 1) of every lane, chains summed in a fixed order
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    f32x4_t v;
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (acc[0][4 * q + e] + acc[1][4 * q + e]) + (acc[2][4 * q + e] + acc[3][4 * q + e]);
-    red[w][q][lane] = v;
-  }
+    for (int q = 0; q < 2; ++q) {
+      f32x4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = acc[mt][0][4 * q + e];
+#pragma unroll
+        for (int ch = 1; ch < C::CH; ++ch) t += acc[mt][ch][4 * q + e];
+        v[e] = t;
+      }
+      red[w][mt][q][lane] = v;
+    }
   __syncthreads();
-  if (w < 2) {  // wave q finishes weight rows 8q + 4hk .. +4 for activation row r32
-    const int q = w;
+  if (w < 2 * MT) {  // wave w finishes weight rows 8q + 4hk .. +4 of tile mt (q = w % 2, mt = w / 2)
+    const int q = w & 1, mt = w >> 1;
     float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int wv = 0; wv < kGvWaves; ++wv) {
-      const f32x4_t v = red[wv][q][lane];
+      const f32x4_t v = red[wv][mt][q][lane];
       a[0] += v[0];
       a[1] += v[1];
       a[2] += v[2];
       a[3] += v[3];
     }
     const int n = n0 + 8 * q + 4 * hk;
-    store4<DTYPE>(p, r32, n, finish4<DTYPE>(a, p, n));
+    store4<DTYPE>(p, 32 * mt + r32, n, finish4<DTYPE>(a, p, n));
   }
 }
 
-// Decode at M <= 4: VALU dot products. The MFMA operand of the kernel above
+template <int DTYPE, int XROWS, int MT>
+static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
+  using C = WsCfg<XROWS, MT>;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+  });
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((int8_gemv_kernel<DTYPE, XROWS, MT>), dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)),
+                     dim3(64 * kGvWaves), C::LDS, stream, p);
+  return hipGetLastError();
+}
+
+// Decode at M <= 2: VALU dot products. The MFMA operand of the kernel above
 // spans 32 activation rows, so at M = 1 it computes 32x the products it
 // keeps and still loads each wave's whole K share before its first MFMA.
 // Here a single-wave workgroup streams kDotRows weight rows in 1 KiB chunks
@@ -466,10 +548,11 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
 // fixed xor butterfly over the 64 lanes then sums every (row, activation row)
 // and lane r * MC + m finishes output (m, n0 + r). Two rows per wave and two
 // chunks ahead measured fastest at M = 1-4 among 1-16 rows and 2-8 chunks
-// (more waves in flight beat deeper per-wave rings).
+// (more waves in flight beat deeper per-wave rings); from M = 3 the MFMA
+// streaming kernel above is faster.
 constexpr int kDotRows = 2;
 constexpr int kDotDepth = 2;
-constexpr int kDotMaxM = 4;  // from M = 5 the MFMA kernel is as fast
+constexpr int kDotMaxM = 2;  // from M = 3 the MFMA streaming kernel is faster
 
 template <int DTYPE, int MC>
 __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p) {
@@ -561,24 +644,19 @@ I8Geom int8_gemm_geometry(int M, int N, int K) {
   I8Geom g{};
   g.n_tiles = (N + kI8BN - 1) / kI8BN;
   g.ksteps = K / kI8BK;
-  if (M <= 32) {  // weight streaming, one launch, no workspace (2: VALU dot products)
+  if (M <= 64) {  // weight streaming, one launch, no workspace (2: VALU dot products)
     g.gemv = M <= kDotMaxM ? 2 : 1;
-    g.mt = 1;
+    g.mt = M <= 32 ? 1 : 2;
     g.m_tiles = 1;
     g.splits = 1;
-    g.m_pad = 32;
+    g.m_pad = 32 * g.mt;
     g.n_pad = g.n_tiles * kI8BN;
     return g;
   }
-  // activation tile: 32 / 64 rows for small M, 128 when that still gives one
-  // (n, m) tile per CU
-  if (M <= 32) g.mt = 1;
-  else if (M <= 64) g.mt = 2;
-  else g.mt = (int64_t)g.n_tiles * ((M + 127) / 128) >= 256 ? 4 : 2;
-  // a single activation tile (decode): the weights stream through, so a deep
-  // ring keeps a workgroup's whole K range in flight; otherwise 3-4 stages
-  // let two workgroups share a CU
-  g.nst = M <= 64 ? 8 : (g.mt >= 4 ? 3 : 4);
+  // activation tile: 128 rows when that still gives one (n, m) tile per CU, else 64
+  g.mt = (int64_t)g.n_tiles * ((M + 127) / 128) >= 256 ? 4 : 2;
+  // 3-4 ring stages let two workgroups share a CU
+  g.nst = g.mt >= 4 ? 3 : 4;
   const int bm = 32 * g.mt;
   g.m_tiles = (M + bm - 1) / bm;
   const int64_t tiles = (int64_t)g.m_tiles * g.n_tiles;
@@ -619,17 +697,15 @@ static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_
   if (g.gemv == 2) {
     const dim3 grid((unsigned)((p.N + kDotRows - 1) / kDotRows));
     if (p.M <= 1) hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 1>), grid, dim3(64), 0, stream, p);
-    else if (p.M <= 2) hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 2>), grid, dim3(64), 0, stream, p);
-    else hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 4>), grid, dim3(64), 0, stream, p);
+    else hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 2>), grid, dim3(64), 0, stream, p);
     return hipGetLastError();
   }
-  if (g.gemv) {
-    hipLaunchKernelGGL(int8_gemv_kernel<DTYPE>, dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)), dim3(64 * kGvWaves),
-                       0, stream, p);
-    return hipGetLastError();
+  if (g.gemv) {  // staged activation rows: 8, 16, 32 or 64
+    if (p.M <= 8) return launch_ws_t<DTYPE, 8, 1>(p, stream);
+    if (p.M <= 16) return launch_ws_t<DTYPE, 16, 1>(p, stream);
+    if (p.M <= 32) return launch_ws_t<DTYPE, 32, 1>(p, stream);
+    return launch_ws_t<DTYPE, 64, 2>(p, stream);
   }
-  if (g.mt == 1 && g.nst == 8) return launch_i8_t<DTYPE, 1, 8>(p, g.lds_bytes, stream);
-  if (g.mt == 2 && g.nst == 8) return launch_i8_t<DTYPE, 2, 8>(p, g.lds_bytes, stream);
   if (g.mt == 2 && g.nst == 4) return launch_i8_t<DTYPE, 2, 4>(p, g.lds_bytes, stream);
   if (g.mt == 4 && g.nst == 3) return launch_i8_t<DTYPE, 4, 3>(p, g.lds_bytes, stream);
   return hipErrorInvalidValue;

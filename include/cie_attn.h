@@ -247,7 +247,8 @@ int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void
  * fp32; the sum is multiplied by the scale once and rounded to x's dtype,
  * then the bias is added in x's dtype (rounded again), as the reference does.
  * workspace: cie_int8_matmul_workspace_bytes(M, N, K) bytes, 16-byte
- * aligned (0 bytes -- NULL allowed -- when the launch does not split K);
+ * aligned (0 bytes -- NULL allowed -- when the launch does not split K,
+ * which is always the case for M <= 64);
  * any contents, not shared by concurrent calls. One kernel is launched on
  * the stream, or two when K is split (the second sums the split partials).
  * Reference: kernels/int8_matmul.py:65-110 (wrapper; bias :107-109) and

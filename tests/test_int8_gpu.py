@@ -53,7 +53,9 @@ def _exact_case(M, N, K, dtype, seed, bias):
                                    (100, 127, 64), (2048, 4096, 256), (515, 1000, 1024), (16, 11008, 4096),
                                    (32, 4096, 11008), (5, 96, 64), (31, 1000, 2112),
                                    # the dot-product kernel (M <= 4): ragged N, K tails within a 1 KiB chunk
-                                   (2, 300, 640), (3, 1001, 2112), (4, 130, 1088), (1, 7, 64), (1, 11008, 4096)])
+                                   (2, 300, 640), (3, 1001, 2112), (4, 130, 1088), (1, 7, 64), (1, 11008, 4096),
+                                   # the streaming kernel at 8 / 16 / 32 / 64 staged rows, K tails within a pass
+                                   (8, 4096, 4096), (12, 520, 1216), (40, 333, 1088), (64, 1000, 4160), (65, 512, 1024)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
     for bias in (False, True):
@@ -96,7 +98,8 @@ def test_layouts_scale_dtypes_and_shapes():
     y = int8_matmul(wide.to(DEV)[:, 32:32 + K], wbig.to(DEV)[:, :K], s.half().to(DEV))
     assert torch.equal(y.cpu(), want.reshape(-1, N))
     assert int8_matmul_workspace_bytes(1, N, 4096) == 0   # weight streaming: one launch, no workspace
-    assert int8_matmul_workspace_bytes(64, N, 4096) > 0   # split K
+    assert int8_matmul_workspace_bytes(64, N, 4096) == 0  # weight streaming up to M = 64
+    assert int8_matmul_workspace_bytes(128, N, 4096) > 0  # split K
 
 
 def test_int8_linear_close_to_float_layer():

@@ -170,7 +170,7 @@ FAKE = 1 << 20
 def _call(**over):
     from engine import _lib
 
-    a = dict(x=FAKE, w=FAKE, s=FAKE, b=None, y=FAKE, xs=4096, wsr=4096, ys=4096, M=64, N=4096, K=4096,
+    a = dict(x=FAKE, w=FAKE, s=FAKE, b=None, y=FAKE, xs=4096, wsr=4096, ys=4096, M=128, N=4096, K=4096,
              dtype=0, sdt=0, ws=FAKE, wsb=1 << 30)
     a.update(over)
     return _lib.load().cie_int8_matmul(a["x"], a["w"], a["s"], a["b"], a["y"], a["xs"], a["wsr"], a["ys"], a["M"],
@@ -194,6 +194,7 @@ def test_int8_matmul_empty_and_workspace_query():
 
     lib = _lib.load()
     assert _call(M=0, x=0, y=0) == 0
-    assert lib.cie_int8_matmul_workspace_bytes(64, 4096, 4096) > 0        # decode shape splits K
+    assert lib.cie_int8_matmul_workspace_bytes(64, 4096, 4096) == 0       # decode shapes stream the weights
+    assert lib.cie_int8_matmul_workspace_bytes(128, 4096, 4096) > 0       # few tiles: split K
     assert lib.cie_int8_matmul_workspace_bytes(4096, 4096, 4096) == 0     # enough tiles: no split
     assert lib.cie_int8_matmul_workspace_bytes(64, 4096, 100) == 0        # unsupported K
