@@ -25,7 +25,7 @@
 // x operand takes x[m_r][16h .. 16h+16) split the same way, so MFMA 0
 // contracts k in {0..7, 16..23} and MFMA 1 k in {8..15, 24..31}.
 //
-// Kernels by M: up to 2 a VALU dot-product kernel, up to 64 a weight-streaming
+// Kernels by M: 1 a VALU dot-product kernel, up to 64 a weight-streaming
 // MFMA kernel (both one launch, no workspace; below), above that the tiled
 // kernel described here.
 //
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParam
   store4<DTYPE>(p, m, n, finish4<DTYPE>(a, p, n));
 }
 
-// Decode-sized layers (2 < M <= 64): weight streaming in one launch. A
+// Decode-sized layers (1 < M <= 64): weight streaming in one launch. A
 // workgroup owns kGvRows = 16 weight rows and its 4 waves split K into
 // quarters. A wave streams its quarter in passes of PG 32-k groups: per pass
 // WI direct-to-LDS loads move the 16 weight rows (32 PG contiguous bytes of
@@ -392,12 +392,18 @@ struct WsCfg {
   static __device__ __forceinline__ int xswz(int row) { return (row / XPH) % XCH; }
 };
 
-template <int DTYPE, int XROWS, int MT>
+// NT16 > 0: the activations as NT16 16-column tiles on v_mfma_f32_16x16x32
+// (A = the 16 weight rows): no discarded A rows, half the weight fragment
+// reads and dequants per k of the 32x32 form (NT16 = 0).
+template <int DTYPE, int XROWS, int MT, int NT16>
 __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
   using E = Elt<DTYPE>;
   using C = WsCfg<XROWS, MT>;
+  constexpr bool M16 = NT16 > 0;
+  constexpr int CH16 = M16 ? (4 / NT16 > 1 ? 4 / NT16 : 1) : 1;  // accumulator chains per 16-column tile
+  static_assert(!M16 || (16 * (NT16 - 1) < XROWS && C::PG % 2 == 0 && NT16 <= kGvWaves), "16-column form");
   extern __shared__ __attribute__((aligned(16))) uint8_t ws_lds[];
-  __shared__ f32x4_t red[kGvWaves][MT][2][64];
+  __shared__ f32x4_t red[kGvWaves][M16 ? NT16 : MT][M16 ? 1 : 2][64];
   const int n0 = blockIdx.x * kGvRows;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -442,11 +448,19 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
       dma16_at(xsrc[i] + 32 * (int64_t)min(gq + xcg[i], G - 1), dst + (uint32_t)C::WBYTES + 1024u * i);
   };
 
-  f32x16 acc[MT][C::CH];
+  f32x16 acc[M16 ? 1 : MT][M16 ? 1 : C::CH];
+  f32x4 acc16[M16 ? NT16 : 1][CH16];
+  if constexpr (M16) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+    for (int t = 0; t < NT16; ++t)
 #pragma unroll
-    for (int ch = 0; ch < C::CH; ++ch) acc[mt][ch] = f32x16{};
+      for (int ch = 0; ch < CH16; ++ch) acc16[t][ch] = f32x4{};
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ch = 0; ch < C::CH; ++ch) acc[mt][ch] = f32x16{};
+  }
 #pragma unroll
   for (int q = 0; q < C::NS; ++q)
     if (q < NP) issue(q);
@@ -459,6 +473,43 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
     else vm_wait<0>();
     const uint8_t* buf = ring_p + (q % C::NS) * C::PASS;
     const int ng = min(C::PG, g1 - g0 - C::PG * q);  // groups of this pass
+    if constexpr (M16) {
+      // lane (i = lane % 16, kq = lane / 16) holds 16 k of weight row i at
+      // 64 h + 16 kq .. +16 (h: 64-k half of the pass) and the same 16 k of
+      // activation row i; the first 8 feed MFMA 0, the last 8 MFMA 1
+      const int i16 = lane & 15, kq = lane >> 4;
+      u32x4 wq[C::PG / 2], xq[NT16][C::PG / 2][2];
+#pragma unroll
+      for (int h = 0; h < C::PG / 2; ++h) {
+        const int wc = 4 * h + kq;
+        wq[h] = *reinterpret_cast<const u32x4*>(buf + i16 * C::WRB + 16 * (wc ^ C::wswz(i16)));
+#pragma unroll
+        for (int t = 0; t < NT16; ++t) {
+          const int xr = min(16 * t + i16, XROWS - 1);
+          const uint8_t* xb = buf + C::WBYTES + xr * C::XRB;
+          const int xc = 8 * h + 2 * kq;
+          xq[t][h][0] = *reinterpret_cast<const u32x4*>(xb + 16 * (xc ^ C::xswz(xr)));
+          xq[t][h][1] = *reinterpret_cast<const u32x4*>(xb + 16 * ((xc + 1) ^ C::xswz(xr)));
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < C::PG / 2; ++h) {
+        if (2 * h < ng) {
+          // the half's second group lies past the range: its lanes (kq >= 2) contribute nothing
+          const u32x4 wv = zero_unless(wq[h], 2 * h + 1 < ng || kq < 2);
+          u32x4 a0, a1;
+          dequant16<DTYPE>(wv, a0, a1);
+#pragma unroll
+          for (int t = 0; t < NT16; ++t) {
+            acc16[t][(2 * h) % CH16] = E::mfma16(a0, xq[t][h][0], acc16[t][(2 * h) % CH16]);
+            acc16[t][(2 * h + 1) % CH16] = E::mfma16(a1, xq[t][h][1], acc16[t][(2 * h + 1) % CH16]);
+          }
+        }
+      }
+      lgkm_wait0();  // this buffer's reads are complete before it is refilled
+      if (q + C::NS < NP) issue(q + C::NS);
+      continue;
+    }
     u32x4 wq[C::PG], xq[MT][C::PG][2];
 #pragma unroll
     for (int gi = 0; gi < C::PG; ++gi) {
@@ -489,6 +540,37 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
     if (q + C::NS < NP) issue(q + C::NS);
   }
   vm_wait<0>();  // no copy into LDS may be in flight when the workgroup ends
+  if constexpr (M16) {
+    // lane (j = lane % 16, iq = lane / 16) of tile t holds weight rows 4 iq .. +4
+    // for activation row 16 t + j; chains summed in a fixed order
+#pragma unroll
+    for (int t = 0; t < NT16; ++t) {
+      f32x4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = acc16[t][0][e];
+#pragma unroll
+        for (int ch = 1; ch < CH16; ++ch) a += acc16[t][ch][e];
+        v[e] = a;
+      }
+      red[w][t][0][lane] = v;
+    }
+    __syncthreads();
+    if (w < NT16) {  // wave t finishes tile t, summing the waves in order
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int wv = 0; wv < kGvWaves; ++wv) {
+        const f32x4_t t = red[wv][w][0][lane];
+        a[0] += t[0];
+        a[1] += t[1];
+        a[2] += t[2];
+        a[3] += t[3];
+      }
+      const int n = n0 + 4 * (lane >> 4);
+      store4<DTYPE>(p, 16 * w + (lane & 15), n, finish4<DTYPE>(a, p, n));
+    }
+    return;
+  }
   // rows 0-15 of each tile: C elements (q = 0, 1) of every lane, chains summed in a fixed order
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -521,22 +603,22 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
   }
 }
 
-template <int DTYPE, int XROWS, int MT>
+template <int DTYPE, int XROWS, int MT, int M16>
 static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
   using C = WsCfg<XROWS, MT>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT>),
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT, M16>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
   });
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((int8_gemv_kernel<DTYPE, XROWS, MT>), dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)),
+  hipLaunchKernelGGL((int8_gemv_kernel<DTYPE, XROWS, MT, M16>), dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)),
                      dim3(64 * kGvWaves), C::LDS, stream, p);
   return hipGetLastError();
 }
 
-// Decode at M <= 2: VALU dot products. The MFMA operand of the kernel above
+// Decode at M = 1: VALU dot products. The MFMA operand of the kernel above
 // spans 32 activation rows, so at M = 1 it computes 32x the products it
 // keeps and still loads each wave's whole K share before its first MFMA.
 // Here a single-wave workgroup streams kDotRows weight rows in 1 KiB chunks
@@ -548,11 +630,11 @@ static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
 // fixed xor butterfly over the 64 lanes then sums every (row, activation row)
 // and lane r * MC + m finishes output (m, n0 + r). Two rows per wave and two
 // chunks ahead measured fastest at M = 1-4 among 1-16 rows and 2-8 chunks
-// (more waves in flight beat deeper per-wave rings); from M = 3 the MFMA
+// (more waves in flight beat deeper per-wave rings); from M = 2 the MFMA
 // streaming kernel above is faster.
 constexpr int kDotRows = 2;
 constexpr int kDotDepth = 2;
-constexpr int kDotMaxM = 2;  // from M = 3 the MFMA streaming kernel is faster
+constexpr int kDotMaxM = 1;  // from M = 2 the MFMA streaming kernel is faster
 
 template <int DTYPE, int MC>
 __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p) {
@@ -696,15 +778,14 @@ template <int DTYPE>
 static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_t stream) {
   if (g.gemv == 2) {
     const dim3 grid((unsigned)((p.N + kDotRows - 1) / kDotRows));
-    if (p.M <= 1) hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 1>), grid, dim3(64), 0, stream, p);
-    else hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 2>), grid, dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 1>), grid, dim3(64), 0, stream, p);
     return hipGetLastError();
   }
   if (g.gemv) {  // staged activation rows: 8, 16, 32 or 64
-    if (p.M <= 8) return launch_ws_t<DTYPE, 8, 1>(p, stream);
-    if (p.M <= 16) return launch_ws_t<DTYPE, 16, 1>(p, stream);
-    if (p.M <= 32) return launch_ws_t<DTYPE, 32, 1>(p, stream);
-    return launch_ws_t<DTYPE, 64, 2>(p, stream);
+    if (p.M <= 8) return launch_ws_t<DTYPE, 8, 1, 1>(p, stream);
+    if (p.M <= 16) return launch_ws_t<DTYPE, 16, 1, 1>(p, stream);
+    if (p.M <= 32) return launch_ws_t<DTYPE, 32, 1, 2>(p, stream);
+    return launch_ws_t<DTYPE, 64, 2, 4>(p, stream);
   }
   if (g.mt == 2 && g.nst == 4) return launch_i8_t<DTYPE, 2, 4>(p, g.lds_bytes, stream);
   if (g.mt == 4 && g.nst == 3) return launch_i8_t<DTYPE, 4, 3>(p, g.lds_bytes, stream);
