@@ -352,16 +352,12 @@ __global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParam
 // of each; rows past M repeat row M - 1), into a private ring of NS pass
 // buffers, so the copies run up to NS - 1 passes ahead of the dequant +
 // MFMA work. Staging the activations through LDS keeps the vector-memory
-// instructions per pass at WI + XI (loading the 32-column MFMA operand per
-// lane took 8 per 128 k, and those loads, not the weight bytes, bounded the
-// kernel). Chunks are XOR-swizzled by row so the fragment reads are
-// conflict-free for the weights and at most 2-way for the activations. The
-// weight rows fill rows 0-15 of the 32-row A operand (rows 16-31 repeat
-// them and are discarded); MT 32-column tiles of activations. MFMAs rotate
-// over 4 / MT accumulators per tile (independent chains, summed in a fixed
-// order); the 4 waves' partial tiles are summed through LDS in wave order
-// (deterministic), then scaled, rounded, stored. Same k permutation as the
-// tiled kernel.
+// instructions per pass at WI + XI (loading the MFMA operand per lane took
+// 8 per 128 k, and those loads, not the weight bytes, bounded the kernel).
+// Chunks are XOR-swizzled by row so the fragment reads spread over the LDS
+// banks. The products run on 16x16x32 MFMAs (see the kernel); the 4 waves'
+// partial tiles are summed through LDS in wave order (deterministic), then
+// scaled, rounded, stored.
 constexpr int kGvWaves = 4;
 constexpr int kGvRows = 16;
 
@@ -382,9 +378,7 @@ struct WsCfg {
   static constexpr int PASS = WBYTES + XROWS * XRB;     // LDS bytes per pass buffer
   static constexpr int NS = XROWS >= 32 ? 3 : 4;        // pass buffers per wave
   static constexpr int PER = WI + XI;                   // copies per pass
-  static constexpr int CH = 4 / MT;                     // accumulator chains per tile
   static constexpr int LDS = kGvWaves * NS * PASS;
-  static_assert(XROWS >= 32 * MT || MT == 1, "staged rows cover the tiles");
   static_assert((NS - 1) * PER < 64, "vmcnt range");
   static_assert(WI * WRI == kGvRows && XI * XRI == XROWS, "copies split evenly");
   // chunk swizzles: rows in one bank phase get distinct chunk positions
@@ -392,28 +386,25 @@ struct WsCfg {
   static __device__ __forceinline__ int xswz(int row) { return (row / XPH) % XCH; }
 };
 
-// NT16 > 0: the activations as NT16 16-column tiles on v_mfma_f32_16x16x32
-// (A = the 16 weight rows): no discarded A rows, half the weight fragment
-// reads and dequants per k of the 32x32 form (NT16 = 0).
+// The activations are NT16 16-column tiles on v_mfma_f32_16x16x32 with the
+// 16 weight rows as the A operand: no discarded A rows (the 32x32x16 form
+// would discard half of them and read twice the weight fragments per k).
 template <int DTYPE, int XROWS, int MT, int NT16>
 __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
   using E = Elt<DTYPE>;
   using C = WsCfg<XROWS, MT>;
-  constexpr bool M16 = NT16 > 0;
-  constexpr int CH16 = M16 ? (4 / NT16 > 1 ? 4 / NT16 : 1) : 1;  // accumulator chains per 16-column tile
-  static_assert(!M16 || (16 * (NT16 - 1) < XROWS && C::PG % 2 == 0 && NT16 <= kGvWaves), "16-column form");
+  constexpr int CH = 4 / NT16 > 1 ? 4 / NT16 : 1;  // accumulator chains per tile
+  static_assert(NT16 >= 1 && NT16 <= kGvWaves && 16 * (NT16 - 1) < XROWS && C::PG % 2 == 0, "tiles");
   extern __shared__ __attribute__((aligned(16))) uint8_t ws_lds[];
-  __shared__ f32x4_t red[kGvWaves][M16 ? NT16 : MT][M16 ? 1 : 2][64];
+  __shared__ f32x4_t red[kGvWaves][NT16][64];
   const int n0 = blockIdx.x * kGvRows;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r32 = lane & 31, hk = lane >> 5;
   const int G = p.K / 32;
   const int g0 = w * G / kGvWaves, g1 = (w + 1) * G / kGvWaves;
   const int NP = (g1 - g0 + C::PG - 1) / C::PG;  // passes of this wave (wave-uniform)
   const uint32_t ring = lds_addr_of(ws_lds) + (uint32_t)(w * C::NS * C::PASS);
   const uint8_t* ring_p = ws_lds + w * C::NS * C::PASS;
-  const int frow = r32 & (kGvRows - 1);  // A-operand row -> weight row of the tile
   // weight copy i: lane -> row WRI i + lane / WCH, stored chunk lane % WCH,
   // which holds chunk (lane % WCH) ^ wswz(row) of the row's pass bytes
   const uint8_t* wsrc[C::WI];
@@ -448,22 +439,18 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
       dma16_at(xsrc[i] + 32 * (int64_t)min(gq + xcg[i], G - 1), dst + (uint32_t)C::WBYTES + 1024u * i);
   };
 
-  f32x16 acc[M16 ? 1 : MT][M16 ? 1 : C::CH];
-  f32x4 acc16[M16 ? NT16 : 1][CH16];
-  if constexpr (M16) {
+  f32x4 acc[NT16][CH];
 #pragma unroll
-    for (int t = 0; t < NT16; ++t)
+  for (int t = 0; t < NT16; ++t)
 #pragma unroll
-      for (int ch = 0; ch < CH16; ++ch) acc16[t][ch] = f32x4{};
-  } else {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int ch = 0; ch < C::CH; ++ch) acc[mt][ch] = f32x16{};
-  }
+    for (int ch = 0; ch < CH; ++ch) acc[t][ch] = f32x4{};
 #pragma unroll
   for (int q = 0; q < C::NS; ++q)
     if (q < NP) issue(q);
+  // lane (i = lane % 16, kq = lane / 16) holds 16 k of weight row i at
+  // 64 h + 16 kq .. +16 (h: 64-k half of the pass) and the same 16 k of
+  // activation row 16 t + i of tile t; the first 8 feed MFMA 0, the last 8 MFMA 1
+  const int i16 = lane & 15, kq = lane >> 4;
   for (int q = 0; q < NP; ++q) {
     // copies issued after pass q's: those of passes q+1 .. min(q+NS-1, NP-1)
     const int ahead = min(C::NS - 1, NP - 1 - q);
@@ -473,66 +460,31 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
     else vm_wait<0>();
     const uint8_t* buf = ring_p + (q % C::NS) * C::PASS;
     const int ng = min(C::PG, g1 - g0 - C::PG * q);  // groups of this pass
-    if constexpr (M16) {
-      // lane (i = lane % 16, kq = lane / 16) holds 16 k of weight row i at
-      // 64 h + 16 kq .. +16 (h: 64-k half of the pass) and the same 16 k of
-      // activation row i; the first 8 feed MFMA 0, the last 8 MFMA 1
-      const int i16 = lane & 15, kq = lane >> 4;
-      u32x4 wq[C::PG / 2], xq[NT16][C::PG / 2][2];
+    u32x4 wq[C::PG / 2], xq[NT16][C::PG / 2][2];
 #pragma unroll
-      for (int h = 0; h < C::PG / 2; ++h) {
-        const int wc = 4 * h + kq;
-        wq[h] = *reinterpret_cast<const u32x4*>(buf + i16 * C::WRB + 16 * (wc ^ C::wswz(i16)));
+    for (int h = 0; h < C::PG / 2; ++h) {
+      const int wc = 4 * h + kq;
+      wq[h] = *reinterpret_cast<const u32x4*>(buf + i16 * C::WRB + 16 * (wc ^ C::wswz(i16)));
+#pragma unroll
+      for (int t = 0; t < NT16; ++t) {
+        const int xr = min(16 * t + i16, XROWS - 1);
+        const uint8_t* xb = buf + C::WBYTES + xr * C::XRB;
+        const int xc = 8 * h + 2 * kq;
+        xq[t][h][0] = *reinterpret_cast<const u32x4*>(xb + 16 * (xc ^ C::xswz(xr)));
+        xq[t][h][1] = *reinterpret_cast<const u32x4*>(xb + 16 * ((xc + 1) ^ C::xswz(xr)));
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < C::PG / 2; ++h) {
+      if (2 * h < ng) {
+        // the half's second group lies past the range: its lanes (kq >= 2) contribute nothing
+        const u32x4 wv = zero_unless(wq[h], 2 * h + 1 < ng || kq < 2);
+        u32x4 a0, a1;
+        dequant16<DTYPE>(wv, a0, a1);
 #pragma unroll
         for (int t = 0; t < NT16; ++t) {
-          const int xr = min(16 * t + i16, XROWS - 1);
-          const uint8_t* xb = buf + C::WBYTES + xr * C::XRB;
-          const int xc = 8 * h + 2 * kq;
-          xq[t][h][0] = *reinterpret_cast<const u32x4*>(xb + 16 * (xc ^ C::xswz(xr)));
-          xq[t][h][1] = *reinterpret_cast<const u32x4*>(xb + 16 * ((xc + 1) ^ C::xswz(xr)));
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < C::PG / 2; ++h) {
-        if (2 * h < ng) {
-          // the half's second group lies past the range: its lanes (kq >= 2) contribute nothing
-          const u32x4 wv = zero_unless(wq[h], 2 * h + 1 < ng || kq < 2);
-          u32x4 a0, a1;
-          dequant16<DTYPE>(wv, a0, a1);
-#pragma unroll
-          for (int t = 0; t < NT16; ++t) {
-            acc16[t][(2 * h) % CH16] = E::mfma16(a0, xq[t][h][0], acc16[t][(2 * h) % CH16]);
-            acc16[t][(2 * h + 1) % CH16] = E::mfma16(a1, xq[t][h][1], acc16[t][(2 * h + 1) % CH16]);
-          }
-        }
-      }
-      lgkm_wait0();  // this buffer's reads are complete before it is refilled
-      if (q + C::NS < NP) issue(q + C::NS);
-      continue;
-    }
-    u32x4 wq[C::PG], xq[MT][C::PG][2];
-#pragma unroll
-    for (int gi = 0; gi < C::PG; ++gi) {
-      const int wc = 2 * gi + hk;
-      wq[gi] = *reinterpret_cast<const u32x4*>(buf + frow * C::WRB + 16 * (wc ^ C::wswz(frow)));
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int xr = min(32 * mt + r32, XROWS - 1);  // B-operand column -> staged activation row
-        const uint8_t* xb = buf + C::WBYTES + xr * C::XRB;
-        const int xc = 4 * gi + 2 * hk;
-        xq[mt][gi][0] = *reinterpret_cast<const u32x4*>(xb + 16 * (xc ^ C::xswz(xr)));
-        xq[mt][gi][1] = *reinterpret_cast<const u32x4*>(xb + 16 * ((xc + 1) ^ C::xswz(xr)));
-      }
-    }
-#pragma unroll
-    for (int gi = 0; gi < C::PG; ++gi) {
-      if (gi < ng) {
-        u32x4 a0, a1;
-        dequant16<DTYPE>(wq[gi], a0, a1);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][(2 * gi) % C::CH] = E::mfma(a0, xq[mt][gi][0], acc[mt][(2 * gi) % C::CH]);
-          acc[mt][(2 * gi + 1) % C::CH] = E::mfma(a1, xq[mt][gi][1], acc[mt][(2 * gi + 1) % C::CH]);
+          acc[t][(2 * h) % CH] = E::mfma16(a0, xq[t][h][0], acc[t][(2 * h) % CH]);
+          acc[t][(2 * h + 1) % CH] = E::mfma16(a1, xq[t][h][1], acc[t][(2 * h + 1) % CH]);
         }
       }
     }
@@ -540,80 +492,47 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
     if (q + C::NS < NP) issue(q + C::NS);
   }
   vm_wait<0>();  // no copy into LDS may be in flight when the workgroup ends
-  if constexpr (M16) {
-    // lane (j = lane % 16, iq = lane / 16) of tile t holds weight rows 4 iq .. +4
-    // for activation row 16 t + j; chains summed in a fixed order
+  // lane (j = lane % 16, iq = lane / 16) of tile t holds weight rows 4 iq .. +4
+  // for activation row 16 t + j; chains summed in a fixed order
 #pragma unroll
-    for (int t = 0; t < NT16; ++t) {
-      f32x4_t v;
+  for (int t = 0; t < NT16; ++t) {
+    f32x4_t v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a = acc16[t][0][e];
+    for (int e = 0; e < 4; ++e) {
+      float a = acc[t][0][e];
 #pragma unroll
-        for (int ch = 1; ch < CH16; ++ch) a += acc16[t][ch][e];
-        v[e] = a;
-      }
-      red[w][t][0][lane] = v;
+      for (int ch = 1; ch < CH; ++ch) a += acc[t][ch][e];
+      v[e] = a;
     }
-    __syncthreads();
-    if (w < NT16) {  // wave t finishes tile t, summing the waves in order
-      float a[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int wv = 0; wv < kGvWaves; ++wv) {
-        const f32x4_t t = red[wv][w][0][lane];
-        a[0] += t[0];
-        a[1] += t[1];
-        a[2] += t[2];
-        a[3] += t[3];
-      }
-      const int n = n0 + 4 * (lane >> 4);
-      store4<DTYPE>(p, 16 * w + (lane & 15), n, finish4<DTYPE>(a, p, n));
-    }
-    return;
+    red[w][t][lane] = v;
   }
-  // rows 0-15 of each tile: C elements (q = 0, 1) of every lane, chains summed in a fixed order
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      f32x4_t v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float t = acc[mt][0][4 * q + e];
-#pragma unroll
-        for (int ch = 1; ch < C::CH; ++ch) t += acc[mt][ch][4 * q + e];
-        v[e] = t;
-      }
-      red[w][mt][q][lane] = v;
-    }
   __syncthreads();
-  if (w < 2 * MT) {  // wave w finishes weight rows 8q + 4hk .. +4 of tile mt (q = w % 2, mt = w / 2)
-    const int q = w & 1, mt = w >> 1;
+  if (w < NT16) {  // wave t finishes tile t, summing the waves in order
     float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int wv = 0; wv < kGvWaves; ++wv) {
-      const f32x4_t v = red[wv][mt][q][lane];
+      const f32x4_t v = red[wv][w][lane];
       a[0] += v[0];
       a[1] += v[1];
       a[2] += v[2];
       a[3] += v[3];
     }
-    const int n = n0 + 8 * q + 4 * hk;
-    store4<DTYPE>(p, 32 * mt + r32, n, finish4<DTYPE>(a, p, n));
+    const int n = n0 + 4 * (lane >> 4);
+    store4<DTYPE>(p, 16 * w + (lane & 15), n, finish4<DTYPE>(a, p, n));
   }
 }
 
-template <int DTYPE, int XROWS, int MT, int M16>
+template <int DTYPE, int XROWS, int MT, int NT16>
 static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
   using C = WsCfg<XROWS, MT>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT, M16>),
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT, NT16>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
   });
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((int8_gemv_kernel<DTYPE, XROWS, MT, M16>), dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)),
+  hipLaunchKernelGGL((int8_gemv_kernel<DTYPE, XROWS, MT, NT16>), dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)),
                      dim3(64 * kGvWaves), C::LDS, stream, p);
   return hipGetLastError();
 }
