@@ -246,12 +246,15 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
 
+  // One barrier per step: it publishes step t and, as every wave has left
+  // step t-1, frees that step's stage, which is refilled at once with step
+  // t + NST - 1 (NST - 1 steps in flight during the compute of step t).
   const int pro = min(C::NST - 1, T);
   for (int t = 0; t < pro; ++t) issue(t);
   for (int t = 0; t < T; ++t) {
+    wait_steps_ahead<C::PER, C::NST - 2>(min(C::NST - 2, T - 1 - t));  // steps issued after step t
+    __syncthreads();  // step t is in LDS for every wave; the stage of step t-1 is free
     if (t + C::NST - 1 < T) issue(t + C::NST - 1);
-    wait_steps_ahead<C::PER, C::NST - 1>(min(C::NST - 1, T - 1 - t));  // steps issued after step t
-    __syncthreads();  // step t is in LDS for every wave
     const uint8_t* st = smem + (t % C::NST) * C::STAGE;
     // every fragment of the step is read first, so the LDS latency is paid
     // once per step rather than in front of each MFMA
@@ -275,7 +278,6 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
         acc[mt] = E::mfma(a1, xb[mt][g2][1], acc[mt]);
       }
     }
-    __syncthreads();  // every wave is done with the slot before it is refilled
   }
 
   // C[i][j] of a 32x32 tile: lane j + 32 * ((i / 4) % 2), element (i / 8) * 4 + i % 4;
