@@ -8,10 +8,30 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdarg>
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "cie_attn.h"
 #include "kernels.hpp"
+
+namespace cie {
+
+hipError_t set_dynamic_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;  // (kernel, device) pairs already set
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kernel, dev})) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert({kernel, dev});
+  return e;
+}
+
+}  // namespace cie
 
 namespace {
 

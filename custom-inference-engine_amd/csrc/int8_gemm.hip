@@ -38,7 +38,6 @@
 // workgroup to finish a tile needs device-coherent stores, an arrival
 // atomic and coherent reloads in series; on MI355X that chain cost more than
 // the second launch.)
-#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -527,12 +526,7 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
 template <int DTYPE, int XROWS, int MT, int NT16>
 static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
   using C = WsCfg<XROWS, MT>;
-  static std::once_flag once;
-  static hipError_t attr = hipSuccess;
-  std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT, NT16>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-  });
+  const hipError_t attr = set_dynamic_lds(reinterpret_cast<const void*>(&int8_gemv_kernel<DTYPE, XROWS, MT, NT16>), C::LDS);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL((int8_gemv_kernel<DTYPE, XROWS, MT, NT16>), dim3((unsigned)((p.N + kGvRows - 1) / kGvRows)),
                      dim3(64 * kGvWaves), C::LDS, stream, p);
@@ -678,12 +672,7 @@ template <int DTYPE, int MT, int NST>
 static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, hipStream_t stream) {
   using C = I8Cfg<MT, NST>;
   if (lds != (size_t)C::NST * C::STAGE) return hipErrorInvalidValue;  // geometry and kernel disagree
-  static std::once_flag once;
-  static hipError_t attr = hipSuccess;
-  std::call_once(once, [&] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, C::NST * C::STAGE);
-  });
+  const hipError_t attr = set_dynamic_lds(reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST>), C::NST * C::STAGE);
   if (attr != hipSuccess) return attr;
   const int nwg = p.n_tiles * p.m_tiles * p.splits;
   hipLaunchKernelGGL((int8_gemm_kernel<DTYPE, MT, NST>), dim3(nwg), dim3(256), lds, stream, p);

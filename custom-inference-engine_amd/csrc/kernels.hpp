@@ -160,6 +160,12 @@ struct I8Geom {
 };
 I8Geom int8_gemm_geometry(int M, int N, int K);
 
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per (kernel, device): the attribute is a property of the kernel as loaded
+// on a device, so a process that launches on several GPUs sets it on each.
+// Thread-safe.
+hipError_t set_dynamic_lds(const void* kernel, int bytes);
+
 hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_int8_gemm(const I8GemmParams& p, const I8Geom& g, int dtype, hipStream_t stream);
 hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, int dtype, int D, hipStream_t stream);

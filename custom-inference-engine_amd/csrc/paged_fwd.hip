@@ -37,7 +37,6 @@
 // [0, ctx_limit] or a block id outside [0, num_blocks) makes that sequence's
 // output NaN.
 #include <climits>
-#include <mutex>
 
 #include "kernels.hpp"
 #include "rope.hpp"
@@ -647,12 +646,7 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
 
 template <int DTYPE, int D>
 static hipError_t launch_paged_t(const PagedParams& p, size_t lds, hipStream_t stream) {
-  static std::once_flag once;
-  static hipError_t attr = hipSuccess;
-  std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kPagedLdsBudget);
-  });
+  const hipError_t attr = set_dynamic_lds(reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D>), kPagedLdsBudget);
   if (attr != hipSuccess) return attr;
   const int64_t n_wg = (int64_t)p.NG * p.Wg;
   hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
