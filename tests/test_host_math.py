@@ -67,7 +67,7 @@ def paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, bs):
     Rt = min(32, R)
     if n_qt > MAX_WAVES:
         return None
-    Hg = max(h for h in range(1, Hk + 1) if Hk % h == 0 and h * D <= 512 and h * n_qt <= MAX_WAVES)
+    Hg = max(h for h in range(1, Hk + 1) if Hk % h == 0 and h * D <= 256 and h * n_qt <= MAX_WAVES)
     NG, NWV, NCH = Hk // Hg, Hg * n_qt, Hg * D // 8
     stage = 2 * TILE * NCH * 16
     dpw = D // 16
