@@ -347,11 +347,8 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     }
   };
 
-  const int pro = min(NST - 1, T);
-  if (issuer)
-    for (int k = 0; k < pro; ++k) issue(k);
-
-  // q rows of the first QPRE sequences, loaded while the first tiles arrive.
+  // q rows of the first QPRE sequences, then the first tiles; the wait below
+  // covers the q loads only (the tile copies issued after them stay in flight)
   const uint16_t* qrow = p.q + hq * p.qs1 + (int64_t)i * p.qs2;
   u32x4 qpre[C::QARR][C::KK];
 #pragma unroll
@@ -360,7 +357,13 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) qpre[e][kk] = load16(qrow + b * p.qs0 + 16 * kk + 8 * hl, rv && e < ne);
   }
-  vm_wait<0>();
+  const int pro = min(NST - 1, T);
+  if (issuer) {
+    for (int k = 0; k < pro; ++k) issue(k);
+    wait_tiles_ahead<C::DPW>(pro);
+  } else {
+    vm_wait<0>();
+  }
   if (p.rope.cos) {  // RoPE fused into the load: row i at position ctx - Lq + i
 #pragma unroll
     for (int e = 0; e < C::QPRE; ++e)
