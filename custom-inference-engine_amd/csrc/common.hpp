@@ -211,6 +211,19 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
   return (const void*)(size_t)(((uint64_t)hi << 32) | lo);
 }
+// Non-temporal forms, for data a kernel streams exactly once (the paged KV
+// pool, INT8 weights): the hint keeps those bytes from displacing the small
+// tensors every workgroup rereads (block tables, lengths, activations) from
+// L2 and the Infinity Cache.
+__device__ __forceinline__ void dma16_sv_nt(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds_addr)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_at_nt(const void* gptr, uint32_t lds_addr) {
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(gptr), "s"(lds_addr) : "memory", "m0");
+}
 __device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, uint32_t lds_addr) {
   lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_addr)

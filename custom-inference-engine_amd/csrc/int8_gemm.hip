@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
     const int gq = g0 + C::PG * q;
     const uint32_t dst = ring + (uint32_t)((q % C::NS) * C::PASS);
 #pragma unroll
-    for (int i = 0; i < C::WI; ++i) dma16_at(wsrc[i] + 32 * (int64_t)min(gq + wcg[i], G - 1), dst + 1024u * i);
+    for (int i = 0; i < C::WI; ++i) dma16_at_nt(wsrc[i] + 32 * (int64_t)min(gq + wcg[i], G - 1), dst + 1024u * i);
 #pragma unroll
     for (int i = 0; i < C::XI; ++i)
       dma16_at(xsrc[i] + 32 * (int64_t)min(gq + xcg[i], G - 1), dst + (uint32_t)C::WBYTES + 1024u * i);
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
     constexpr int s = decltype(S)::value;
     const int k = min(1024 * c + 16 * lane, p.K - 16);
 #pragma unroll
-    for (int r = 0; r < kDotRows; ++r) wq[s][r] = *reinterpret_cast<const u32x4*>(wrow[r] + k);
+    for (int r = 0; r < kDotRows; ++r) wq[s][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + k));
 #pragma unroll
     for (int m = 0; m < MC; ++m) {
       xq[s][m][0] = load16_clamped(xrow[m] + k);
