@@ -23,6 +23,13 @@ namespace cie {
 
 constexpr int kAppendUnroll = 4;  // chunks per thread per trip, all loads in flight together
 
+// The pool rows are written once: those stores carry the non-temporal hint
+// (a 4 x 2048-token append in 6.9 us instead of 8.9). The new rows are read
+// with ordinary loads, which leave them in the caches for the prefill
+// attention that reads the same K/V next (non-temporal loads made the
+// append-then-attention section 3.5 % slower); the dense rotated copy of K
+// (k_out), read by that attention too, is written normally.
+
 __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
   const int b = blockIdx.y;
   const int n0 = p.cu_new[b];
@@ -63,8 +70,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
 #pragma unroll
     for (int u = 0; u < kAppendUnroll; ++u) {
       if (ok[u]) {
-        *reinterpret_cast<u32x4*>(p.kc + dk[u]) = kv[u];
-        *reinterpret_cast<u32x4*>(p.vc + dv[u]) = vv[u];
+        __builtin_nontemporal_store(kv[u], reinterpret_cast<u32x4*>(p.kc + dk[u]));
+        __builtin_nontemporal_store(vv[u], reinterpret_cast<u32x4*>(p.vc + dv[u]));
       }
     }
   }
@@ -135,10 +142,10 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(const AppendParams 
     for (int u = 0; u < kRopeUnroll; ++u) {
       rope8<DTYPE>(klo[u], khi[u], cs[u], sn[u]);
       if (ok[u]) {
-        *reinterpret_cast<u32x4*>(p.kc + dk[u]) = klo[u];
-        *reinterpret_cast<u32x4*>(p.kc + dk[u] + half) = khi[u];
-        *reinterpret_cast<u32x4*>(p.vc + dv[u]) = vlo[u];
-        *reinterpret_cast<u32x4*>(p.vc + dv[u] + half) = vhi[u];
+        __builtin_nontemporal_store(klo[u], reinterpret_cast<u32x4*>(p.kc + dk[u]));
+        __builtin_nontemporal_store(khi[u], reinterpret_cast<u32x4*>(p.kc + dk[u] + half));
+        __builtin_nontemporal_store(vlo[u], reinterpret_cast<u32x4*>(p.vc + dv[u]));
+        __builtin_nontemporal_store(vhi[u], reinterpret_cast<u32x4*>(p.vc + dv[u] + half));
       }
       if (p.k_out && in[u]) {
         *reinterpret_cast<u32x4*>(p.k_out + dout[u]) = klo[u];

@@ -31,12 +31,12 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
     bad |= !ok;
     const int64_t tr = (ok ? (int64_t)pos : 0) * HALF + 8 * j;
     const uint16_t* x = p.x + (int64_t)b * p.xs0 + (int64_t)h * p.xs1 + (int64_t)l * p.xs2 + 8 * j;
-    u32x4 lo = *reinterpret_cast<const u32x4*>(x);
-    u32x4 hi = *reinterpret_cast<const u32x4*>(x + HALF);
+    u32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x));  // streamed once
+    u32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + HALF));
     rope8<DTYPE>(lo, hi, tab8(p.tab.cos + tr), tab8(p.tab.sin + tr));
     if (!ok) lo = hi = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
     uint16_t* o = p.out + (int64_t)b * p.os0 + (int64_t)h * p.os1 + (int64_t)l * p.os2 + 8 * j;
-    *reinterpret_cast<u32x4*>(o) = lo;
+    *reinterpret_cast<u32x4*>(o) = lo;  // cached: attention reads the rotated rows next
     *reinterpret_cast<u32x4*>(o + HALF) = hi;
   }
   if (p.status && __builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(p.status, 2u);
