@@ -627,7 +627,12 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
   g.NCH = g.Hg * D / 8;
   const size_t stage = (size_t)2 * kPagedTile * g.NCH * 16;  // K and V tiles
   const int dpw = D / 16;
-  int nst = (int)std::min<size_t>(4, kPagedLdsBudget / stage);
+  // Ring budget: decode-like shapes (few query rows per kv head, little
+  // compute per tile) run best as two workgroups per CU with two stages
+  // each; verify-like ones as one workgroup with three (decode_b32 -3 %,
+  // verify_b8 -1.4 % against four stages for both).
+  const size_t budget = g.R <= 8 ? 75 * 1024 : 100 * 1024;
+  int nst = (int)std::min<size_t>(4, std::min<size_t>(budget, kPagedLdsBudget) / stage);
   nst = std::min(std::max(nst, 2), 1 + 31 / dpw);  // 2 * dpw * (nst - 1) copies fit vmcnt
   g.NST = nst;
   g.lds_bytes = (size_t)nst * stage;

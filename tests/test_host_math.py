@@ -71,7 +71,8 @@ def paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, bs):
     NG, NWV, NCH = Hk // Hg, Hg * n_qt, Hg * D // 8
     stage = 2 * TILE * NCH * 16
     dpw = D // 16
-    nst = min(max(min(4, LDS_BUDGET // stage), 2), 1 + 31 // dpw)
+    budget = 75 * 1024 if R <= 8 else 100 * 1024
+    nst = min(max(min(4, min(budget, LDS_BUDGET) // stage), 2), 1 + 31 // dpw)
     lds = nst * stage
     static = 4 * (IDS + 8 * ENTRIES) + 16
     wpc = max(1, min((160 * 1024) // (lds + static), 16 // NWV))
