@@ -12,9 +12,12 @@
 // flight while two are resident; one workgroup barrier per tile both publishes
 // the next tile and frees the stage that is refilled next.
 // Per tile and wave:
-//   S^T[BN x 32] = K_tile . Q_w^T     MFMA 32x32x16; A = ds_read_b128 of K rows,
-//                                      B = Q^T resident in registers
-//   mask + running max (one v_permlane32_swap), p = exp2(s*c - m), c = scale*log2e
+//   S^T[BN x 32] = K_tile . Q_w^T - m MFMA 32x32x16; A = ds_read_b128 of K rows,
+//                                      B = Q^T resident in registers, scaled by
+//                                      c = scale*log2e; one more k-block holds
+//                                      a constant column (A) against -m (B)
+//   p = exp2(s)                        the whole softmax argument comes out of
+//                                      the MFMA: no per-score VALU arithmetic
 //   O^T[D x 32] += V^T_tile . P^T      MFMA 32x32x16; A = ds_read_b64_tr_b16 of
 //                                      the row-major V tile, B = P^T straight
 //                                      from the S^T registers
@@ -23,8 +26,11 @@
 // wave's diagonal or the key tail; a workgroup stops at the last key any of
 // its rows can see (the n_end bound of kernels/flash_attention.py:75-77).
 //
-// The running max is refreshed lazily and without a per-tile row max: p(t)
-// is computed against the reference max m, and only when a lane's 32
+// Q is scaled by c once, as it is loaded, and rounded to the input type
+// (relative error 2^-11 for fp16, 2^-8 for bf16 per element, far inside the
+// output tolerances; c * q must be finite in the input type); m is kept at a
+// value the 16-bit B operand holds exactly. The running max is refreshed lazily and without a per-tile row
+// max: p(t) is computed against the reference max m, and only when a lane's 32
 // probabilities of the tile sum past 2^10 (so some p may not fit the 16-bit
 // P.V operand; always the case for a row that had no visible key before)
 // does the wave recompute S(t) from the still-resident K tile, take its row
@@ -56,6 +62,17 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// The two 16-bit values of a packed pair as floats (exact).
+template <int DTYPE>
+__device__ __forceinline__ f32x2 unpack2(uint32_t v) {
+  if constexpr (DTYPE == 0) {
+    const f16x2 h = __builtin_bit_cast(f16x2, v);
+    return f32x2{(float)h[0], (float)h[1]};
+  } else {
+    return f32x2{__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u)};
+  }
 }
 
 template <int D>
@@ -112,8 +129,8 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   const int q0w = mt * C::BM + wave * 32;  // first row of this wave
   const int qi = q0w + l32;                // row owned by this lane
 
-  // Q^T as the B operand: lane holds Q[qi][16kk + 8hl .. +8] (sign-flipped
-  // when the caller's scale is negative, so c below is never negative).
+  // Q^T as the B operand: lane holds c * Q[qi][16kk + 8hl .. +8] (c takes the
+  // sign of the caller's scale; p.scale_log2 itself is never negative).
   const uint16_t* qrow = p.q + b * p.qs0 + hq * p.qs1 + (int64_t)qi * p.qs2;
   u32x4 qf[C::KK];
 #pragma unroll
@@ -121,8 +138,17 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   if (p.rope.cos)  // RoPE fused into the load: row qi at position q_pos0[b] + qi
     rope_q_lane<DTYPE, D>(qf, p.rope.cos, p.rope.sin, p.rope.rows, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq,
                           hl);
+  const float c = p.scale_log2;
+  {
+    const float cq = p.q_sign ? -c : c;
 #pragma unroll
-  for (int kk = 0; kk < C::KK; ++kk) qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
+    for (int kk = 0; kk < C::KK; ++kk)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const f32x2 v = unpack2<DTYPE>(qf[kk][w]);
+        qf[kk][w] = E::pack2(v[0] * cq, v[1] * cq);
+      }
+  }
 
   // Key range of the workgroup and of this wave; lim = last key this row sees.
   const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;
@@ -136,7 +162,6 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   const int lim = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + qi) : p.Lk - 1;
   const int wave_lim0 = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + q0w) : p.Lk - 1;  // smallest lim in the wave
   const int n_tiles = (kend + BN - 1) / BN;
-  const float c = p.scale_log2;
 
   const uint16_t* kb = p.k + b * p.ks0 + kvh * p.ks1;
   const uint16_t* vb = p.v + b * p.vs0 + kvh * p.vs1;
@@ -226,6 +251,19 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
   float m = -INFINITY, l = 0.f;
+  // Extra k-block of the QK^T product: A[key][0] = kMScale, B[0][row] =
+  // -m / kMScale, every other entry 0, so the accumulator starts at -m.
+  constexpr float kMScale = DTYPE == 0 ? 256.f : 1.f;  // fp16 range for |m| up to 2^24
+  const u32x4 a_one = {hl == 0 ? E::pack2(kMScale, 0.f) : 0u, 0u, 0u, 0u};
+  u32x4 b_m = {0u, 0u, 0u, 0u};
+  auto set_m = [&](float x) CIE_INLINE {  // m = x rounded to what the B operand holds exactly
+    if (x != -INFINITY) {
+      x = fminf(x, 65504.f * kMScale);
+      x = unpack2<DTYPE>(E::pack2(x * (1.f / kMScale), 0.f))[0] * kMScale;
+    }
+    m = x;
+    b_m[0] = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
+  };
 
   vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
   const int pro = min(C::NST - 1, n_tiles);
@@ -241,7 +279,10 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     __syncthreads();
     qk(0, sc);
     mask(0, sc);
-    m = xhalf_max(rowmax(sc)) * c;  // the reference max starts at tile 0's row max
+    set_m(xhalf_max(rowmax(sc)));  // the reference max starts at tile 0's row max
+    const float sub = m == -INFINITY ? 0.f : m;
+#pragma unroll
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) sc[mt2] -= sub;
   }
   const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
   // One pipeline step: sc holds S(t), S(t+1) is produced in sn; ST is the
@@ -256,7 +297,6 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
       if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
     }
     if (t * BN >= wave_kend) return;  // wave-uniform: every row of the wave is done
-    const float neg_m = m == -INFINITY ? 0.f : -m;
 
     // (c) S(t+1) on the MFMA pipe, P(t) on the VALU, interleaved by hand:
     // after each QK MFMA the next EPC elements of S(t) become probabilities.
@@ -281,7 +321,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
         ka[i] = *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
       }
 #pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = f32x16{};
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = E::mfma(a_one, b_m, f32x16{});
       constexpr int EPC = 16 * C::MT / C::NQK;  // S(t) elements per MFMA
 #pragma unroll
       for (int i = 0; i < C::NQK; ++i) {
@@ -291,7 +331,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 #pragma unroll
         for (int e = i * EPC; e < (i + 1) * EPC; ++e) {
           const int m2 = e / 16, ee = e % 16;
-          sc[m2][ee] = exp2_fast(fmaf(sc[m2][ee], c, neg_m));
+          sc[m2][ee] = exp2_fast(sc[m2][ee]);
           if (ee & 1) {  // a pair is complete: pack it and add it to the row sum
             const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
             asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
@@ -311,23 +351,24 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // to the row max, accumulators rescaled, the tile's p recomputed.
     float ts = ts0 + ts1;
     if (__builtin_amdgcn_ballot_w64(!(ts <= kSumTrigger))) {
+      const float m_in = m == -INFINITY ? 0.f : m;  // subtracted from S(t+1) in sn
       qk(t, sc);
       mask(t, sc);
-      const float mxs = xhalf_max(rowmax(sc)) * c;
-      const bool grow = mxs > m;
-      const float m_new = grow ? mxs : m;
-      const float alpha = grow ? exp2_fast(m - m_new) : 1.f;  // 0 when m was -inf
+      const float m_old = m;
+      set_m(maxf(m, xhalf_max(rowmax(sc))));
+      const float alpha = m > m_old ? exp2_fast(m_old - m) : 1.f;  // 0 when m was -inf
       l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
-      m = m_new;
       const float nm = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] += m_in + nm;
       ts0 = 0.f;
       ts1 = 0.f;
 #pragma unroll
       for (int e = 0; e < 16 * C::MT; e += 2) {
         const int m2 = e / 16, ee = e % 16;
-        const uint32_t pk = E::pack2(exp2_fast(fmaf(sc[m2][ee], c, nm)), exp2_fast(fmaf(sc[m2][ee + 1], c, nm)));
+        const uint32_t pk = E::pack2(exp2_fast(sc[m2][ee] + nm), exp2_fast(sc[m2][ee + 1] + nm));
         pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
         if (ee & 2) ts1 = E::sum2(pk, ts1);
         else ts0 = E::sum2(pk, ts0);

@@ -151,7 +151,7 @@ struct I8GemmParams {
 // Launch geometry of an INT8 GEMM; a pure function of (M, N, K), so the
 // workspace query and the launch agree.
 struct I8Geom {
-  int gemv;                // 1: weight-streaming MFMA kernel (M <= 32), 2: VALU dot kernel (M = 1); one launch
+  int gemv;                // 1: weight-streaming MFMA kernel (M <= 64), 2: VALU dot kernel (M = 1); one launch
   int mt;                  // 32-row activation tiles per workgroup
   int nst;                 // LDS ring stages
   int m_tiles, n_tiles, ksteps, splits, m_pad, n_pad;
