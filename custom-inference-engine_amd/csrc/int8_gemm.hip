@@ -650,8 +650,12 @@ I8Geom int8_gemm_geometry(int M, int N, int K) {
     g.n_pad = g.n_tiles * kI8BN;
     return g;
   }
-  // activation tile: 128 rows when that still gives one (n, m) tile per CU, else 64
-  g.mt = (int64_t)g.n_tiles * ((M + 127) / 128) >= 256 ? 4 : 2;
+  // activation tile: the larger of 128 / 64 rows that gives two (n, m) tiles
+  // per CU; failing both, 128 rows when that gives one tile per CU, else 64
+  // (N = K = 4096: M = 1024 ran 47.3 us at 64 rows against 52.1 at 128; at
+  // M = 512, 32-row tiles or a K split for two tiles per CU were slower)
+  const int64_t t128 = (int64_t)g.n_tiles * ((M + 127) / 128), t64 = (int64_t)g.n_tiles * ((M + 63) / 64);
+  g.mt = t128 >= 512 ? 4 : (t64 >= 512 ? 2 : (t128 >= 256 ? 4 : 2));
   // 3-4 ring stages let two workgroups share a CU
   g.nst = g.mt >= 4 ? 3 : 4;
   const int bm = 32 * g.mt;

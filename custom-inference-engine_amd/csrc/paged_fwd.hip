@@ -158,10 +158,11 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   const uint32_t nan2 = 0x7fff7fffu;  // NaN in both fp16 and bf16
 
   // ---- schedule: every wave derives it from the context lengths ----------
-  int NT = 0;
+  int NT = 0, ctx0 = 0;  // ctx0: this lane's length among the first 64 sequences, reused below
   for (int b0 = 0; b0 < p.B; b0 += 64) {
     const int b = b0 + lane;
     const int ctx = b < p.B ? p.lens[b] : 0;
+    if (b0 == 0) ctx0 = ctx;
     NT += ctx_valid(p, ctx) ? (ctx + kPagedTile - 1) / kPagedTile : 0;
   }
   NT = wave_sum_i(NT);
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   for (int b0 = 0; b0 < p.B; b0 += 64) {
     if (j != 0 && carry >= S1) break;
     const int b = b0 + lane;
-    const int ctx = b < p.B ? p.lens[b] : 0;
+    const int ctx = b0 == 0 ? ctx0 : (b < p.B ? p.lens[b] : 0);
     const bool valid = ctx_valid(p, ctx);
     const int t = valid ? (ctx + kPagedTile - 1) / kPagedTile : 0;
     const int incl = wave_incl_scan(t, lane);
