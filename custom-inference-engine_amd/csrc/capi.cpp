@@ -268,6 +268,9 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   p.block_size = block_size;
   p.ctx_limit = ctx_limit;
   p.bsdiv = cie::make_fastdiv((uint32_t)block_size);
+  p.rtdiv = cie::make_fastdiv((uint32_t)g.Rt);
+  p.nwvdiv = cie::make_fastdiv((uint32_t)g.NWV);
+  p.ngdiv = cie::make_fastdiv((uint32_t)g.NG);
   {
     // Largest element offset of either pool from its base, and the 24-bit
     // multiplier bounds of the narrow address path.

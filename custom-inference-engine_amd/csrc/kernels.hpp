@@ -64,6 +64,7 @@ struct PagedParams {
   int narrow;     // pool offsets < 2^31 elements, ids and block/offset strides < 2^24
   uint32_t ks0_24, ks1_24, vs0_24, vs1_24;
   FastDiv bsdiv;
+  FastDiv rtdiv, nwvdiv, ngdiv;  // item decomposition of the merge pass
   int Hg, NG, n_qt, NWV, NCH, NST, Wg;
   float scale_log2;  // |scale| * log2(e), never below 1e-30
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative

@@ -66,19 +66,24 @@ __device__ __forceinline__ int row_swizzle(int nch, int t) {
   return nch >= 16 ? bitrev4(t & 15) : nch == 8 ? bitrev3((t >> 1) & 7) : nch == 4 ? ((t >> 2) & 3) : ((t >> 3) & 1);
 }
 
-__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
+// Inclusive prefix sum over the 64 lanes: DPP row shifts within each row of
+// 16 lanes, then the row totals broadcast forward (row_bcast:15 into rows 1
+// and 3, row_bcast:31 into rows 2 and 3). Lanes whose DPP source lies
+// outside the row, and rows outside the row mask, add the old value 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return x;
 }
 
-__device__ __forceinline__ int wave_sum_i(int x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  return x;
+// floor(n / d) for n < 2^63, 0 < d < 2^31: a 32-bit division whenever n fits
+// in 32 bits (always, unless tiles x workgroups reaches 2^32).
+__device__ __forceinline__ int div_small(uint64_t n, uint32_t d) {
+  return n <= 0xffffffffull ? (int)((uint32_t)n / d) : (int)(n / d);
 }
 
 __device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
@@ -88,7 +93,7 @@ __device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
 // Range index of tile x when nt tiles are cut into wg <= nt ranges
 // [floor(j nt / wg), floor((j+1) nt / wg)).
 __device__ __forceinline__ int range_of(int x, int nt, int wg) {
-  return (int)(((int64_t)(x + 1) * wg - 1) / nt);
+  return div_small((uint64_t)(x + 1) * (uint32_t)wg - 1, (uint32_t)nt);
 }
 
 template <int DPW>
@@ -158,19 +163,21 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   const uint32_t nan2 = 0x7fff7fffu;  // NaN in both fp16 and bf16
 
   // ---- schedule: every wave derives it from the context lengths ----------
-  int NT = 0, ctx0 = 0;  // ctx0: this lane's length among the first 64 sequences, reused below
+  // ctx0, incl0: this lane's length and inclusive tile prefix among the
+  // first 64 sequences, reused below
+  int NT = 0, ctx0 = 0, incl0 = 0;
   for (int b0 = 0; b0 < p.B; b0 += 64) {
     const int b = b0 + lane;
     const int ctx = b < p.B ? p.lens[b] : 0;
-    if (b0 == 0) ctx0 = ctx;
-    NT += ctx_valid(p, ctx) ? (ctx + kPagedTile - 1) / kPagedTile : 0;
+    const int incl = wave_incl_scan(ctx_valid(p, ctx) ? (ctx + kPagedTile - 1) / kPagedTile : 0);
+    if (b0 == 0) ctx0 = ctx, incl0 = incl;
+    NT += __builtin_amdgcn_readlane(incl, 63);
   }
-  NT = wave_sum_i(NT);
   // W <= NT ranges, so none is empty: every range a sequence spans holds one
   // of its pieces (workgroups j >= W have nothing to do).
   const int W = min(p.Wg, NT);
-  const int S0 = j < W ? (int)((int64_t)j * NT / W) : NT;
-  const int S1 = j < W ? (int)((int64_t)(j + 1) * NT / W) : NT;
+  const int S0 = j < W ? div_small((uint64_t)j * (uint32_t)NT, (uint32_t)W) : NT;
+  const int S1 = j < W ? div_small((uint64_t)(j + 1) * (uint32_t)NT, (uint32_t)W) : NT;
 
   int ne = 0, nid = 0, carry = 0;
   for (int b0 = 0; b0 < p.B; b0 += 64) {
@@ -179,9 +186,9 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const int ctx = b0 == 0 ? ctx0 : (b < p.B ? p.lens[b] : 0);
     const bool valid = ctx_valid(p, ctx);
     const int t = valid ? (ctx + kPagedTile - 1) / kPagedTile : 0;
-    const int incl = wave_incl_scan(t, lane);
+    const int incl = b0 == 0 ? incl0 : wave_incl_scan(t);
     const int pre = carry + incl - t;
-    carry += __shfl(incl, 63);
+    carry += __builtin_amdgcn_readlane(incl, 63);
     if (j == 0) {
       // Sequences without tiles: zeros for an empty history, NaN for an
       // invalid length. The first workgroup of each head group writes them.
@@ -206,7 +213,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
       const int blk_hi = (int)fdiv((uint32_t)(min(ctx, kPagedTile * tt_hi) - 1), p.bsdiv);
       nids = blk_hi - blk_lo + 1;
     }
-    const int ids_incl = wave_incl_scan(nids, lane);
+    const int ids_incl = wave_incl_scan(nids);
     const uint64_t om = __builtin_amdgcn_ballot_w64(ov);
     if (w == 0 && ov) {
       const int e = ne + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(om >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)om, 0));
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
       if (pre >= S0) p.info[(int64_t)gh * p.B + b] = int4{j, j1 - j0 + 1, pre > S0 ? 1 : 0, 0};
     }
     ne += __builtin_popcountll(om);
-    nid += __shfl(ids_incl, 63);
+    nid += __builtin_amdgcn_readlane(ids_incl, 63);
   }
   const int T = S1 - S0;
 
@@ -540,20 +547,60 @@ __device__ __forceinline__ void merge_state(float& M, float& L, float4& A, float
   M = Mn;
 }
 
+// Value of lane (lane ^ OFF) for OFF = 1, 2, 4, by DPP: quad permutations for
+// 1 and 2, the two row rotations by 4 (row_ror:12 reads lane + 4, row_ror:4
+// reads lane - 4 within each row of 16) for 4.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float x) {
+  const int v = __float_as_int(x);
+  if constexpr (OFF == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+  } else if constexpr (OFF == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, false));  // quad_perm [2,3,0,1]
+  } else {
+    static_assert(OFF == 4, "lane_xor: 1, 2 or 4");
+    const int up = __builtin_amdgcn_mov_dpp(v, 0x12c, 0xf, 0xf, false);  // row_ror:12
+    const int dn = __builtin_amdgcn_mov_dpp(v, 0x124, 0xf, 0xf, false);  // row_ror:4
+    return __int_as_float((threadIdx.x & 4) ? dn : up);
+  }
+}
+
+template <int OFF>
+__device__ __forceinline__ void butterfly_step(int t, float& M, float& L, float4& A) {
+  const float m2 = lane_xor<OFF>(M), l2 = lane_xor<OFF>(L);
+  const float4 a2 = {lane_xor<OFF>(A.x), lane_xor<OFF>(A.y), lane_xor<OFF>(A.z), lane_xor<OFF>(A.w)};
+  // the lower lane of each pair keeps its own state first: same order in both lanes
+  if (t & OFF) {
+    float Mx = m2, Lx = l2;
+    float4 Ax = a2;
+    merge_state(Mx, Lx, Ax, M, L, A);
+    M = Mx, L = Lx, A = Ax;
+  } else {
+    merge_state(M, L, A, m2, l2, a2);
+  }
+}
+
 template <int DTYPE, int D>
 __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   using E = Elt<DTYPE>;
   constexpr int Q4 = D / 4;
-  const int t = threadIdx.x % kMergeLanes;
-  int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) / kMergeLanes;
+  static_assert(kMergeLanes == 8, "the butterfly below covers eight lanes");
+  // thread index < 2^31 (paged_geometry bounds the merge grid): 32-bit
+  // decomposition, invariant divisors by multiply-shift
+  const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  const int t = (int)(tid % kMergeLanes);
+  uint32_t item = tid / kMergeLanes;
   const int d4 = (int)(item % Q4);
   item /= Q4;
-  const int row = (int)(item % p.Rt);
-  item /= p.Rt;
-  const int w = (int)(item % p.NWV);
-  item /= p.NWV;
-  const int gh = (int)(item % p.NG);
-  const int b = (int)(item / p.NG);
+  uint32_t qn = fdiv(item, p.rtdiv);
+  const int row = (int)(item - qn * (uint32_t)p.Rt);
+  item = qn;
+  qn = fdiv(item, p.nwvdiv);
+  const int w = (int)(item - qn * (uint32_t)p.NWV);
+  item = qn;
+  qn = fdiv(item, p.ngdiv);
+  const int gh = (int)(item - qn * (uint32_t)p.NG);
+  const int b = (int)qn;
   // Items of one wave belong to at most a few sequences; lanes past the end
   // or without work still take part in the shuffles below.
   const bool in = b < p.B;
@@ -583,20 +630,9 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
         if (k0 + kMergeLanes * u < pieces) merge_state(M, L, A, ml[u].x, ml[u].y, a[u]);
     }
   }
-#pragma unroll
-  for (int off = 1; off < kMergeLanes; off <<= 1) {
-    const float m2 = __shfl_xor(M, off), l2 = __shfl_xor(L, off);
-    const float4 a2 = {__shfl_xor(A.x, off), __shfl_xor(A.y, off), __shfl_xor(A.z, off), __shfl_xor(A.w, off)};
-    // the lower lane of each pair keeps its own state first: same order in both lanes
-    if (t & off) {
-      float Mx = m2, Lx = l2;
-      float4 Ax = a2;
-      merge_state(Mx, Lx, Ax, M, L, A);
-      M = Mx, L = Lx, A = Ax;
-    } else {
-      merge_state(M, L, A, m2, l2, a2);
-    }
-  }
+  butterfly_step<1>(t, M, L, A);
+  butterfly_step<2>(t, M, L, A);
+  butterfly_step<4>(t, M, L, A);
   if (!act || t != 0) return;
   const int g = r / p.Lq, i = r - g * p.Lq;
   const int hq = (gh * p.Hg + hh) * p.group + g;
@@ -651,6 +687,10 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
     return g;
   }
   g.Wg = (int)wg;
+  if ((int64_t)B * g.NG * g.NWV * g.Rt * (D / 4) * kMergeLanes >= ((int64_t)1 << 31)) {
+    g.err = "problem too large for one launch";
+    return g;
+  }
   g.info_bytes = ((size_t)g.NG * B * sizeof(int4) + 255) / 256 * 256;
   g.slot_bytes = (size_t)g.NG * g.Wg * 2 * g.NWV * g.Rt * (D + 2) * sizeof(float);
   g.ok = 1;
