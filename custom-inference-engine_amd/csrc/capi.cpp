@@ -495,7 +495,8 @@ int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int6
     return fail(CIE_EINVAL, "invalid sizes (B=%d, H=%d, L=%d, pos_batch_stride=%lld)", B, H, L,
                 (long long)pos_batch_stride);
   CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
-  const int64_t total = (int64_t)B * H * L * (D / 16);
+  const int nhg = (H + cie::kRopeHeads - 1) / cie::kRopeHeads;
+  const int64_t total = (int64_t)B * nhg * L * (D / 16);
   if (total >= ((int64_t)1 << 31)) return fail(CIE_EINVAL, "too many rows for one launch");
   if (total == 0) {
     g_err.clear();
@@ -515,9 +516,10 @@ int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int6
   p.tab = cie::RopeTables{rope_cos, rope_sin, rope_rows};
   p.status = status;
   p.B = B; p.H = H; p.L = L;
+  p.NHG = nhg;
   p.total = (uint32_t)total;
   p.ldiv = cie::make_fastdiv((uint32_t)L);
-  p.hdiv = cie::make_fastdiv((uint32_t)H);
+  p.hgdiv = cie::make_fastdiv((uint32_t)nhg);
   return launch_status(cie::launch_rope(p, dtype, D, static_cast<hipStream_t>(stream)));
 }
 

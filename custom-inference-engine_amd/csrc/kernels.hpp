@@ -132,9 +132,11 @@ struct RopeParams {
   RopeTables tab;
   uint32_t* status;    // optional: 2 ORed in when a position is outside the table
   int B, H, L;
-  uint32_t total;      // B * H * L * D / 16 chunk pairs
-  FastDiv ldiv, hdiv;
+  int NHG;             // head groups of kRopeHeads heads: ceil(H / kRopeHeads)
+  uint32_t total;      // B * NHG * L * D / 16 (one thread per chunk pair of a head group)
+  FastDiv ldiv, hgdiv;
 };
+constexpr int kRopeHeads = 8;  // heads one thread rotates (they share the position's table row)
 
 // INT8-weight GEMM: y (M, N) = (x (M, K) . w (N, K)^T) * scales[n] (+ bias[n]).
 struct I8GemmParams {
