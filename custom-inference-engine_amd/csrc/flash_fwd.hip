@@ -8,9 +8,10 @@
 //
 // Memory path: each K/V tile (BN keys) is copied global -> LDS by 16-byte
 // direct-to-LDS loads issued by all four waves (no VGPR staging), row-major
-// with the 16-byte chunks of each row XOR-swizzled (chunk_swizzle). NST-2 tiles are in
-// flight while two are resident; one workgroup barrier per tile both publishes
-// the next tile and frees the stage that is refilled next.
+// with the 16-byte chunks of each row XOR-swizzled (chunk_swizzle). Up to two tiles are in
+// flight while the tiles being read stay resident; one workgroup barrier per
+// tile (four stages), or per two tiles at D=128 (five stages), publishes the
+// next tile(s) and frees the stage(s) refilled next.
 // Per tile and wave:
 //   S^T[BN x 32] = K_tile . Q_w^T - m MFMA 32x32x16; A = ds_read_b128 of K rows,
 //                                      B = Q^T resident in registers, scaled by
@@ -85,7 +86,10 @@ struct FlashCfg {
   static constexpr int MT = BN / 32;                               // 32-key score tiles
   static constexpr int TILE = BN * D;                              // elements of one tensor tile
   static constexpr int STAGE = 2 * TILE;                           // K tile, then V tile
-  static constexpr int NST = D == 256 ? 3 : 4;                     // 2 resident + NST-2 in flight
+  // pipeline steps per workgroup barrier: two at D=128 (1.1 % faster at
+  // S=16384), one elsewhere (D=64: two were 3 % slower)
+  static constexpr int PAIR = D == 128 ? 2 : 1;
+  static constexpr int NST = D == 256 ? 3 : (PAIR == 2 ? 5 : 4);   // ring stages (see the tile loop)
   static constexpr int NW = BN * S / 256;                          // 1 KiB copies per wave per tensor
   static constexpr int PER_TILE = 2 * NW;                          // copies per wave per tile
   static constexpr int OCC = D <= 128 ? 2 : 1;                     // workgroups per CU
@@ -266,13 +270,19 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   };
 
   vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
-  const int pro = min(C::NST - 1, n_tiles);
+  const int pro = min(C::PAIR == 2 ? C::NST - 2 : C::NST - 1, n_tiles);
   for (int t = 0; t < pro; ++t) issue(t);
 
   // Software pipeline: iteration t holds S(t) in registers, computes
-  // S(t+1) = K(t+1) Q^T while turning S(t) into P(t), then O += V(t) P(t).
-  // Tiles t and t+1 are resident; the copies of the next NST-2 tiles are in
-  // flight.
+  // S(t+1) = K(t+1) Q^T while turning S(t) into P(t), then O += V(t) P(t),
+  // so tiles t and t+1 are read. With PAIR = 2 (D=128, five stages) one barrier
+  // serves two steps: at even t every wave waits for its copies of tiles
+  // t+1 and t+2 (all it has in flight), the barrier publishes them, and the
+  // stages of tiles t-2 and t-1 (finished by every wave once it passes the
+  // barrier) are refilled with tiles t+3 and t+4; tiles t, t+1, t+2 stay
+  // resident for steps t and t+1. With PAIR = 1 (four stages; three at
+  // D=256) each step waits for tile t+1, the barrier publishes it, and the
+  // stage of tile t-1 is refilled.
   f32x16 sc[C::MT];
   if (n_tiles > 0) {
     wait_ahead<C::NST, C::PER_TILE>(pro - 1);
@@ -289,9 +299,16 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   // ring stage of tile t (t % NST). The loop below runs U steps per trip with
   // the two score arrays swapped each step, so the scores are never copied
   // between registers.
-  auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
+  auto step = [&](auto ST, auto EVEN, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
     constexpr int st = decltype(ST)::value, st1 = (st + 1) % C::NST;
-    if (t + 1 < n_tiles) {
+    if constexpr (C::PAIR == 2) {
+      if (decltype(EVEN)::value && t + 1 < n_tiles) {
+        vm_wait<0>();
+        __syncthreads();  // tiles t+1, t+2 resident for all waves; stages of t-2, t-1 free
+        if (t + 3 < n_tiles) issue(t + 3);
+        if (t + 4 < n_tiles) issue(t + 4);
+      }
+    } else if (t + 1 < n_tiles) {
       wait_ahead<C::NST, C::PER_TILE>(min(C::NST - 3, n_tiles - 2 - t));
       __syncthreads();  // tile t+1 resident for all waves; stage of tile t-1 free
       if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
@@ -404,13 +421,15 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     }
   };
   f32x16 sb[C::MT];
-  constexpr int U = C::NST % 2 == 0 ? C::NST : 2 * C::NST;  // steps per trip: stage and score buffer both repeat
+  // steps per trip: stage, score buffer and barrier parity all repeat
+  constexpr int U = C::NST % 2 == 0 ? C::NST : 2 * C::NST;
   for (int t = 0; t < n_tiles; t += U) {
     static_for<U>([&](auto I) CIE_INLINE {
       constexpr int i = decltype(I)::value;
+      using Even = std::integral_constant<bool, i % 2 == 0>;
       if (t + i < n_tiles) {
-        if constexpr (i % 2 == 0) step(std::integral_constant<int, i % C::NST>{}, t + i, sc, sb);
-        else step(std::integral_constant<int, i % C::NST>{}, t + i, sb, sc);
+        if constexpr (i % 2 == 0) step(std::integral_constant<int, i % C::NST>{}, Even{}, t + i, sc, sb);
+        else step(std::integral_constant<int, i % C::NST>{}, Even{}, t + i, sb, sc);
       }
     });
   }
