@@ -75,6 +75,19 @@ def test_sweep(D, dtype, causal, shape):
     assert_close(out, ref, TOL[dtype], f"D={D} {dtype} causal={causal} {shape}")
 
 
+@pytest.mark.parametrize("L", [1, 31, 32, 33, 64, 65, 96, 97, 128, 160, 161, 192, 193, 224])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_d128_every_tile_count(L, dtype, causal):
+    """D=128 streams 32-key tiles and publishes them two per workgroup
+    barrier: 1..7 tiles, full and ragged, cover both barrier parities at
+    the last tile and every prologue length."""
+    q, k, v = _inputs(1, 4, 2, L, L, 128, dtype, seed=1000 + L, vscale=0.5)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=causal)
+    assert_close(out, ref, TOL[dtype], f"D=128 L={L} {dtype} causal={causal}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_more_queries_than_keys_gives_nan_rows(dtype):
     q, k, v = _inputs(1, 4, 2, 150, 20, 64, dtype, seed=5, vscale=0.5)
