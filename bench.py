@@ -59,8 +59,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="run only a 256 MiB copy (counter calibration) and the prefill kernel, "
-                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+                    help="run only a 256 MiB copy (counter calibration), the prefill kernel and the "
+                         "paged decode / verify pairs, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     return ap.parse_args()
 
 
@@ -94,6 +94,13 @@ def traffic_probe():
     for _ in range(3):
         fl()
     torch.cuda.synchronize()
+    del fl
+    for name in ("decode_b32", "verify_b8"):  # the paged pair, three launches each on distinct pool copies
+        pl = PagedLaunch(workloads.WORKLOADS[name](), dev)
+        for i in range(3):
+            pl(i)
+        torch.cuda.synchronize()
+        del pl
     print("traffic probe done", flush=True)
 
 
