@@ -348,7 +348,8 @@ def _captured(fn):
 def decode_step_times(dev, iters=20):
     """One layer's attention section for a decode step of the decode_b32 shape
     (32 sequences, contexts 256..4096, 32/8 heads, D=64, fp16): the batched
-    paged path (append_batch + paged attention, one launch each) against the
+    paged path (the append fused into the paged attention launch pair; also
+    timed as a separate append launch before it) against the
     reference's per-sequence structure (append, gather of the whole history,
     dense causal attention; engine/model/block.py:57-71), both on the GPU."""
     import torch
@@ -378,6 +379,9 @@ def decode_step_times(dev, iters=20):
     def paged(i=0):
         attention_section(q, k, v, 0, cache, step)
 
+    def paged_two_launch(i=0):
+        attention_section(q, k, v, 0, cache, step, fuse_append=False)
+
     def paged_rope(i=0):
         attention_section(q, k, v, 0, cache, step, rope=emb.tables)
 
@@ -389,6 +393,7 @@ def decode_step_times(dev, iters=20):
 
     # the same section captured once in a HIP graph and replayed (no host work per layer)
     graph = _captured(paged)
+    graph_two = _captured(paged_two_launch)
     graph_rope = _captured(paged_rope)
     graph_rope_unfused = _captured(paged_rope_unfused)
 
@@ -401,12 +406,14 @@ def decode_step_times(dev, iters=20):
 
     t_paged = event_time_ms(paged, iters, 3)
     t_graph = event_time_ms(lambda i=0: graph.replay(), iters, 3)
+    t_graph_two = event_time_ms(lambda i=0: graph_two.replay(), iters, 3)
     t_graph_rope = event_time_ms(lambda i=0: graph_rope.replay(), iters, 3)
     t_graph_rope_unfused = event_time_ms(lambda i=0: graph_rope_unfused.replay(), iters, 3)
     t_ref = event_time_ms(per_sequence, max(3, iters // 4), 1)
-    del graph, graph_rope, graph_rope_unfused, cache
+    del graph, graph_two, graph_rope, graph_rope_unfused, cache
     torch.cuda.empty_cache()
     return {"us": round(t_paged * 1e3, 2), "graph_replay_us": round(t_graph * 1e3, 2),
+            "graph_replay_append_then_paged_us": round(t_graph_two * 1e3, 2),
             "graph_replay_rope_fused_us": round(t_graph_rope * 1e3, 2),
             "graph_replay_rope_apply_then_section_us": round(t_graph_rope_unfused * 1e3, 2),
             "per_sequence_gather_path_us": round(t_ref * 1e3, 1), "speedup": round(t_ref / t_paged, 1)}

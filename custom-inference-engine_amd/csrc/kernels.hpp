@@ -70,6 +70,13 @@ struct PagedParams {
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
   int causal;
   RopeTables rope;  // rotate q row i of sequence b at position lens[b] - Lq + i as it is loaded
+  // Fused append (kn != nullptr): the Lq newest tokens of sequence b are rows
+  // b * Lq + i of kn / vn ((B * Lq, Hk, D), strides kns0 / vns0 per token,
+  // kns1 / vns1 per head). Attention reads them from there, and the
+  // workgroup whose range holds a new token writes it into the pool.
+  const uint16_t* kn;
+  const uint16_t* vn;
+  int64_t kns0, kns1, vns0, vns1;
 };
 
 constexpr int kPagedTile = 32;         // tokens per tile
@@ -132,11 +139,13 @@ struct RopeParams {
   RopeTables tab;
   uint32_t* status;    // optional: 2 ORed in when a position is outside the table
   int B, H, L;
-  int NHG;             // head groups of kRopeHeads heads: ceil(H / kRopeHeads)
+  int HG;              // heads one thread rotates: kRopeHeads, or 1 for launches too small to fill the GPU
+  int NHG;             // head groups: ceil(H / HG)
   uint32_t total;      // B * NHG * L * D / 16 (one thread per chunk pair of a head group)
   FastDiv ldiv, hgdiv;
 };
 constexpr int kRopeHeads = 8;  // heads one thread rotates (they share the position's table row)
+constexpr int64_t kRopeGroupMin = (int64_t)512 * 256 * kRopeHeads;  // chunk pairs from which 8-head threads still give 512 workgroups
 
 // INT8-weight GEMM: y (M, N) = (x (M, K) . w (N, K)^T) * scales[n] (+ bias[n]).
 struct I8GemmParams {

@@ -87,7 +87,8 @@ __device__ __forceinline__ int div_small(uint64_t n, uint32_t d) {
 }
 
 __device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
-  return ctx >= 0 && ctx <= p.ctx_limit && (ctx == 0 || p.num_blocks > 0);
+  // with a fused append the Lq new tokens are part of every valid context
+  return ctx >= (p.kn ? p.Lq : 0) && ctx <= p.ctx_limit && (ctx == 0 || p.num_blocks > 0);
 }
 
 // Range index of tile x when nt tiles are cut into wg <= nt ranges
@@ -270,6 +271,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   // (P % NCH) ^ row_swizzle(token) of the token's group row.
   int ltok[C::DPW];
   int64_t goffk[C::DPW], goffv[C::DPW];
+  int64_t gnk[C::DPW], gnv[C::DPW];  // the same chunk in a new-token row (fused append)
 #pragma unroll
   for (int x = 0; x < C::DPW; ++x) {
     const int P = 64 * (hh * C::DPW + x) + lane;
@@ -278,6 +280,8 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const int hd = c / C::S, dc = c % C::S;
     ltok[x] = tk;
     goffk[x] = (int64_t)(gh * p.Hg + hd) * p.ks2 + 8 * dc;
+    gnk[x] = (int64_t)(gh * p.Hg + hd) * p.kns1 + 8 * dc;
+    gnv[x] = (int64_t)(gh * p.Hg + hd) * p.vns1 + 8 * dc;
     goffv[x] = (int64_t)(gh * p.Hg + hd) * p.vs2 + 8 * dc;
   }
   // Fragment reads: K row l32 (chunk 2 kk + hl of head hh), V^T rows.
@@ -294,6 +298,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
 
   // Issue cursor.
   int ie = 0, i_base = 0, i_end = __builtin_amdgcn_readfirstlane(ent[0][3]);
+  int i_b = __builtin_amdgcn_readfirstlane(ent[0][0]);
   int i_ctx = __builtin_amdgcn_readfirstlane(ent[0][1]), i_ttlo = __builtin_amdgcn_readfirstlane(ent[0][2]);
   int i_idb = __builtin_amdgcn_readfirstlane(ent[0][4]), i_blk = __builtin_amdgcn_readfirstlane(ent[0][5]);
   int i_stage = 0;
@@ -315,10 +320,34 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
       i_ttlo = __builtin_amdgcn_readfirstlane(ent[ie][2]);
       i_idb = __builtin_amdgcn_readfirstlane(ent[ie][4]);
       i_blk = __builtin_amdgcn_readfirstlane(ent[ie][5]);
+      i_b = __builtin_amdgcn_readfirstlane(ent[ie][0]);
     }
     const int tbase = kPagedTile * (i_ttlo + k - i_base);
     const uint32_t st = ring_lds + 2u * (uint32_t)(i_stage * STAGE_EL) + 1024u * (uint32_t)(hh * C::DPW);
     i_stage = i_stage + 1 == NST ? 0 : i_stage + 1;
+    if (p.kn && tbase + kPagedTile > i_ctx - p.Lq) {
+      // a tile holding new tokens: those rows come from kn / vn, the rest
+      // from the pool (per-lane addresses)
+#pragma unroll
+      for (int x = 0; x < C::DPW; ++x) {
+        const int tk = min(tbase + ltok[x], i_ctx - 1);
+        const uint16_t *sk, *sv;
+        if (tk >= i_ctx - p.Lq) {
+          const int64_t row = (int64_t)i_b * p.Lq + (tk - (i_ctx - p.Lq));
+          sk = p.kn + row * p.kns0 + gnk[x];
+          sv = p.vn + row * p.vns0 + gnv[x];
+        } else {
+          const int blk = (int)fdiv((uint32_t)tk, p.bsdiv);
+          const int off = tk - blk * p.block_size;
+          const int bid = max(sbt[i_idb + blk - i_blk], 0);
+          sk = p.kc + (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 + goffk[x];
+          sv = p.vc + (int64_t)bid * p.vs0 + (int64_t)off * p.vs1 + goffv[x];
+        }
+        dma16_at_nt(sk, st + 1024u * x);
+        dma16_at_nt(sv, st + 2u * TILE_EL + 1024u * x);
+      }
+      return;
+    }
     if (row_copies) {
 #pragma unroll
       for (int x = 0; x < C::DPW; ++x) {
@@ -522,6 +551,38 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
       }
     }
     __syncthreads();  // every wave is done with this stage before it is refilled
+  }
+
+  // Fused append: the new tokens inside this range go into the pool, the
+  // head group's rows of each (16-byte chunks over the whole workgroup).
+  // Nothing in this launch reads those pool rows (the tiles holding them
+  // took the rows from kn / vn), so no ordering is needed.
+  if (p.kn) {
+    const int cpr = p.Hg * (D / 8);  // chunks of one tensor per token row of the head group
+    for (int e = 0; e < ne; ++e) {
+      const int ctx = ent[e][1], tt_lo = ent[e][2], n = ent[e][3], idb = ent[e][4], blk_lo = ent[e][5];
+      const int lo = max(ctx - p.Lq, kPagedTile * tt_lo), hi = min(ctx, kPagedTile * (tt_lo + n));
+      const int b = ent[e][0];
+      for (int u = threadIdx.x; u < (hi > lo ? hi - lo : 0) * cpr * 2; u += blockDim.x) {
+        const int tsr = u / (2 * cpr), rem = u - tsr * 2 * cpr;
+        const int tensor = rem / cpr, c = rem - tensor * cpr;
+        const int pos = lo + tsr;
+        const int blk = (int)fdiv((uint32_t)pos, p.bsdiv);
+        const int bid = sbt[idb + blk - blk_lo];
+        if (bid < 0) continue;  // invalid block id: the output is NaN, nothing is written
+        const int off = pos - blk * p.block_size;
+        const int h = gh * p.Hg + c / (D / 8), d = 8 * (c % (D / 8));
+        const int64_t row = (int64_t)b * p.Lq + (pos - (ctx - p.Lq));
+        if (tensor == 0)
+          *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.kc) + (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 +
+                                    (int64_t)h * p.ks2 + d) =
+              *reinterpret_cast<const u32x4*>(p.kn + row * p.kns0 + (int64_t)h * p.kns1 + d);
+        else
+          *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.vc) + (int64_t)bid * p.vs0 + (int64_t)off * p.vs1 +
+                                    (int64_t)h * p.vs2 + d) =
+              *reinterpret_cast<const u32x4*>(p.vn + row * p.vns0 + (int64_t)h * p.vns1 + d);
+      }
+    }
   }
 
 }

@@ -4,9 +4,10 @@
 // with positions (L,), (B, L) or the default 0..L-1.
 //
 // One thread rotates one chunk pair (x[j*8 .. +8), x[D/2 + j*8 .. +8)) of
-// one position l in each of up to kRopeHeads heads: the fp32 cos/sin row
-// chunks of the position (read through L2) are loaded once for all of them,
-// and the thread's 2 * kRopeHeads row loads are in flight together.
+// one position l in each of up to HG heads (HG = kRopeHeads for launches
+// large enough to keep 512 workgroups, else 1): the fp32 cos/sin row chunks
+// of the position (read through L2) are loaded once for all of them, and
+// the thread's 2 * HG row loads are in flight together.
 // Consecutive threads take consecutive chunk pairs of a row, then the next
 // position, so for every head the loads and stores of a wave cover
 // contiguous row halves. A position outside the table yields NaN for the
@@ -17,11 +18,10 @@
 
 namespace cie {
 
-template <int DTYPE, int D>
+template <int DTYPE, int D, int HG>
 __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
   constexpr uint32_t UPR = D / 16;  // chunk pairs per row
   constexpr int HALF = D / 2;
-  constexpr int HG = kRopeHeads;
   const uint32_t stride = gridDim.x * 256u;
   bool bad = false;
   for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u < p.total; u += stride) {
@@ -59,17 +59,24 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
   if (p.status && __builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(p.status, 2u);
 }
 
-template <int DTYPE>
-static hipError_t launch_rope_d(const RopeParams& p, int D, int grid, hipStream_t stream) {
+template <int DTYPE, int HG>
+static hipError_t launch_rope_g(const RopeParams& p, int D, int grid, hipStream_t stream) {
   switch (D) {
-    case 16: hipLaunchKernelGGL((rope_kernel<DTYPE, 16>), dim3(grid), dim3(256), 0, stream, p); break;
-    case 32: hipLaunchKernelGGL((rope_kernel<DTYPE, 32>), dim3(grid), dim3(256), 0, stream, p); break;
-    case 64: hipLaunchKernelGGL((rope_kernel<DTYPE, 64>), dim3(grid), dim3(256), 0, stream, p); break;
-    case 128: hipLaunchKernelGGL((rope_kernel<DTYPE, 128>), dim3(grid), dim3(256), 0, stream, p); break;
-    case 256: hipLaunchKernelGGL((rope_kernel<DTYPE, 256>), dim3(grid), dim3(256), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((rope_kernel<DTYPE, 16, HG>), dim3(grid), dim3(256), 0, stream, p); break;
+    case 32: hipLaunchKernelGGL((rope_kernel<DTYPE, 32, HG>), dim3(grid), dim3(256), 0, stream, p); break;
+    case 64: hipLaunchKernelGGL((rope_kernel<DTYPE, 64, HG>), dim3(grid), dim3(256), 0, stream, p); break;
+    case 128: hipLaunchKernelGGL((rope_kernel<DTYPE, 128, HG>), dim3(grid), dim3(256), 0, stream, p); break;
+    case 256: hipLaunchKernelGGL((rope_kernel<DTYPE, 256, HG>), dim3(grid), dim3(256), 0, stream, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int DTYPE>
+static hipError_t launch_rope_d(const RopeParams& p, int D, int grid, hipStream_t stream) {
+  if (p.HG == kRopeHeads) return launch_rope_g<DTYPE, kRopeHeads>(p, D, grid, stream);
+  if (p.HG == 1) return launch_rope_g<DTYPE, 1>(p, D, grid, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_rope(const RopeParams& p, int dtype, int D, hipStream_t stream) {

@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "cie_rope_apply",
     "cie_flash_fwd_rope",
     "cie_paged_fwd_rope",
+    "cie_paged_fwd_append",
     "cie_kv_append_rope",
     "cie_int8_matmul_workspace_bytes",
     "cie_int8_matmul",
@@ -84,6 +85,11 @@ def _declare(lib: ctypes.CDLL) -> None:
                                        _i, _i, _i, _i, _i, _i, _i, _i, _i,
                                        ctypes.c_float, _i, _i, _vp, _vp, _i, _vp]
     lib.cie_paged_fwd_rope.restype = _i
+    lib.cie_paged_fwd_append.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                                         _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
+                                         _i, _i, _i, _i, _i, _i, _i, _i, _i,
+                                         ctypes.c_float, _i, _i, _vp]
+    lib.cie_paged_fwd_append.restype = _i
     lib.cie_kv_append_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                        _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i64p, _vp]
     lib.cie_kv_append_rope.restype = _i

@@ -183,6 +183,7 @@ def paged_attention(
     *,
     rope: tuple[torch.Tensor, torch.Tensor] | None = None,
     out: torch.Tensor | None = None,
+    new_kv: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Attention of the newest ``Lq`` tokens of each sequence over its paged
     KV history.
@@ -204,6 +205,15 @@ def paged_attention(
     b is rotated at position ``context_lens[b] - Lq + i`` as it is loaded,
     bit-identical to ``rope_apply`` on q first. ``out``: an existing
     (B, Hq, Lq, D) tensor to write, as in :func:`flash_attention`.
+
+    ``new_kv``: (k_new, v_new), each (B * Lq, Hk, D) with row b * Lq + i =
+    new token i of sequence b, already rotated, not yet in the pool. The
+    append happens in the same launch pair (``cie_paged_fwd_append``):
+    attention reads those rows directly and writes them into the pool at
+    positions ``context_lens[b] - Lq + i``, so the pool and the result equal
+    ``kv_append`` followed by ``paged_attention`` bit for bit. Every context
+    must count its Lq new tokens (a shorter one gives NaN rows). Not
+    combined with ``rope``.
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_tables", block_tables), ("context_lens", context_lens)):
@@ -228,6 +238,16 @@ def paged_attention(
         raise ValueError(f"context_lens must be (B,), got {tuple(context_lens.shape)}")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    if new_kv is not None:
+        if rope is not None:
+            raise ValueError("paged_attention: new_kv takes K already rotated; rope cannot be combined with it")
+        k_new, v_new = new_kv
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            if not t.is_cuda or t.device != q.device:
+                raise RuntimeError(f"paged_attention requires CUDA tensors on one device ({name})")
+            if tuple(t.shape) != (B * Lq, Hk, D) or t.dtype != q.dtype:
+                raise ValueError(f"{name} must be ({B * Lq}, {Hk}, {D}) in {q.dtype}, got {tuple(t.shape)} {t.dtype}")
+        k_new, v_new = _kernel_layout(k_new), _kernel_layout(v_new)
 
     lib = _lib.load()
     bt = block_tables.to(torch.int32).contiguous()
@@ -250,7 +270,13 @@ def paged_attention(
             B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc,
             float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype])
     with torch.cuda.device(q.device):
-        if rope is None:
+        if new_kv is not None:
+            rc = lib.cie_paged_fwd_append(q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(),
+                                          v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(), out.data_ptr(),
+                                          workspace.data_ptr(), ws_have, _lib.strides(q), _lib.strides3(k_new),
+                                          _lib.strides3(v_new), _lib.strides(k_cache), _lib.strides(v_cache),
+                                          _lib.strides(out), *args[12:], stream)
+        elif rope is None:
             rc = lib.cie_paged_fwd(*args, stream)
         else:
             rc = lib.cie_paged_fwd_rope(*args, *rope_args(rope, D, q.device), stream)

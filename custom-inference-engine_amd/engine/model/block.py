@@ -36,7 +36,8 @@ _PAGED_MAX_ROWS = 256  # query rows per kv head one paged launch takes
 
 
 def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_idx: int, cache: PagedKVCache,
-                      step: StepBatch, rope: tuple[torch.Tensor, torch.Tensor] | None = None) -> torch.Tensor:
+                      step: StepBatch, rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+                      fuse_append: bool = True) -> torch.Tensor:
     """q: (B, Hq, L, D), k/v: (B, Hk, L, D): the L new tokens of each
     sequence, at positions ``starts[b] + 0..L-1``, after RoPE when ``rope``
     is None, before it when ``rope`` is the model's (cos, sin) tables
@@ -44,7 +45,12 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
     L, starts)``, made once per engine step before the first layer: it
     allocates the blocks, extends the lengths (so the history includes the
     new tokens, as in the reference, which appends before it attends) and
-    holds the step's device metadata. Returns (B, L, Hq * D)."""
+    holds the step's device metadata. Returns (B, L, Hq * D).
+
+    With ``fuse_append`` (default) a step whose new tokens are the newest of
+    every sequence and whose K is already rotated (``rope`` None) appends
+    inside the paged attention launch pair (``paged_attention(new_kv=...)``),
+    bit-identical to ``append_step`` followed by ``paged_attention``."""
     B, Hq, L, D = q.shape
     if step.context_lens.shape[0] != B or k.shape[0] != B or v.shape[0] != B or step.num_new != L:
         raise ValueError(f"step of {step.context_lens.shape[0]} sequences x {step.num_new} tokens "
@@ -70,6 +76,11 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
             cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope, k_out=k_rot)
             flash_attention(q, k_rot.view(B, L, Hk, D).transpose(1, 2), v, causal=True, scale=scale, rope=rope,
                             out=out)  # positions 0..L-1
+    elif (Hq // Hk) * L <= _PAGED_MAX_ROWS and rope is None and fuse_append and step.aligned:
+        cache._validate(k_rows)
+        cache._validate(v_rows)
+        paged_attention(q, cache.k[layer_idx], cache.v[layer_idx], step.block_tables, step.context_lens,
+                        causal=True, scale=scale, max_context=step.max_context, out=out, new_kv=(k_rows, v_rows))
     elif (Hq // Hk) * L <= _PAGED_MAX_ROWS:
         cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope)
         q_rope = rope

@@ -216,6 +216,33 @@ int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
                        void* stream);
 
 /*
+ * cie_kv_append followed by cie_paged_fwd in one launch pair, for new tokens
+ * that are the Lq newest positions of every context (context_lens[b]
+ * already counts them, as after the reference's append). k_new, v_new:
+ * (B * Lq, Hk, D), row b * Lq + i = new token i of sequence b, strides
+ * {token, head} in elements (multiples of 8), unit head_dim stride,
+ * 16-byte aligned. Attention reads those rows straight from k_new / v_new;
+ * each is also written into the pool at position context_lens[b] - Lq + i
+ * through the block table, so the pool afterwards equals what cie_kv_append
+ * leaves, and o equals cie_kv_append then cie_paged_fwd bit for bit.
+ * A context shorter than Lq is invalid here (NaN output, nothing written);
+ * a token whose block id is out of range is not written (its sequence's
+ * output is NaN, as in cie_paged_fwd). K must already be rotated (no RoPE
+ * is applied to it). Same workspace as cie_paged_fwd.
+ * Reference: engine/model/block.py:57-71 (append, then gather + attend).
+ */
+int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
+                         const void* k_cache, const void* v_cache,
+                         const int32_t* block_tables, const int32_t* context_lens,
+                         void* o, void* workspace, size_t workspace_bytes,
+                         const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
+                         const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,
+                         int B, int Hq, int Hk, int Lq, int D,
+                         int num_blocks, int block_size, int max_blocks_per_seq,
+                         int max_context, float scale, int causal, int dtype,
+                         void* stream);
+
+/*
  * cie_kv_append with RoPE fused into the write of K: k_new holds the
  * projected, un-rotated keys; token i of sequence b is rotated at position
  * start[b] + i, then written (V is copied as is). k_out (optional, may be
