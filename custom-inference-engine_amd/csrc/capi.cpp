@@ -358,6 +358,25 @@ int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
                     kn_stride, vn_stride);
 }
 
+int cie_paged_fwd_append_rope(const void* q, const void* k_new, const void* v_new,
+                              const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              void* o, void* workspace, size_t workspace_bytes,
+                              const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
+                              const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,
+                              int B, int Hq, int Hk, int Lq, int D,
+                              int num_blocks, int block_size, int max_blocks_per_seq,
+                              int max_context, float scale, int causal, int dtype,
+                              const float* rope_cos, const float* rope_sin, int rope_rows,
+                              void* stream) {
+  if (!k_new || !v_new) return fail(CIE_EINVAL, "k_new / v_new: NULL pointer");
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
+                    kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
+                    max_context, scale, causal, dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, k_new,
+                    v_new, kn_stride, vn_stride);
+}
+
 }  // extern "C"
 
 static int append_impl(const void* k_new, const void* v_new, void* k_cache, void* v_cache,

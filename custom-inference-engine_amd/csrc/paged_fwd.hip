@@ -471,6 +471,31 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const uint16_t* vst = kst + TILE_EL;
     c_stage = c_stage + 1 == NST ? 0 : c_stage + 1;
     const int t0 = kPagedTile * (c_ttlo + n - c_base);
+    if (p.kn && p.rope.cos && t0 + kPagedTile > c_ctx - p.Lq) {
+      // fused append with RoPE: the new K rows of this tile arrived
+      // unrotated from kn; rotate them in LDS at their positions (pairs of
+      // 16-byte chunks j, j + D/16 of each head, found through the row
+      // swizzle), then publish the rotated tile
+      const int first = max(c_ctx - p.Lq, t0), last = min(c_ctx, t0 + kPagedTile);
+      const int items = (last - first) * p.Hg * (D / 16);
+      for (int u = threadIdx.x; u < items; u += blockDim.x) {
+        const int tr = u / (p.Hg * (D / 16)), rem = u - tr * p.Hg * (D / 16);
+        const int hd = rem / (D / 16), jj = rem - hd * (D / 16);
+        const int pos = first + tr, t = pos - t0;
+        const int sw = row_swizzle(NCH, t);
+        uint16_t* rowp = const_cast<uint16_t*>(kst) + (t << lg_nch) * 8;
+        u32x4* lo = reinterpret_cast<u32x4*>(rowp + ((hd * C::S + jj) ^ sw) * 8);
+        u32x4* hi = reinterpret_cast<u32x4*>(rowp + ((hd * C::S + jj + C::S / 2) ^ sw) * 8);
+        u32x4 a = *lo, b = *hi;
+        const bool ok = pos < p.rope.rows;
+        const int64_t tr0 = (ok ? (int64_t)pos : 0) * (D / 2) + 8 * jj;
+        rope8<DTYPE>(a, b, tab8(p.rope.cos + tr0), tab8(p.rope.sin + tr0));
+        if (!ok) a = b = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
+        *lo = a;
+        *hi = b;
+      }
+      __syncthreads();
+    }
 
     f32x16 sc = f32x16{};
 #pragma unroll
@@ -559,6 +584,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   // took the rows from kn / vn), so no ordering is needed.
   if (p.kn) {
     const int cpr = p.Hg * (D / 8);  // chunks of one tensor per token row of the head group
+    const bool rot = p.rope.cos != nullptr;
     for (int e = 0; e < ne; ++e) {
       const int ctx = ent[e][1], tt_lo = ent[e][2], n = ent[e][3], idb = ent[e][4], blk_lo = ent[e][5];
       const int lo = max(ctx - p.Lq, kPagedTile * tt_lo), hi = min(ctx, kPagedTile * (tt_lo + n));
@@ -573,7 +599,20 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         const int off = pos - blk * p.block_size;
         const int h = gh * p.Hg + c / (D / 8), d = 8 * (c % (D / 8));
         const int64_t row = (int64_t)b * p.Lq + (pos - (ctx - p.Lq));
-        if (tensor == 0)
+        if (tensor == 0 && rot) {
+          // K rotated at its position: the thread of the pair's first chunk writes both
+          if (d >= D / 2) continue;
+          const uint16_t* src = p.kn + row * p.kns0 + (int64_t)h * p.kns1 + d;
+          u32x4 a = *reinterpret_cast<const u32x4*>(src), bb = *reinterpret_cast<const u32x4*>(src + D / 2);
+          const bool ok = pos < p.rope.rows;
+          const int64_t tr0 = (ok ? (int64_t)pos : 0) * (D / 2) + d;
+          rope8<DTYPE>(a, bb, tab8(p.rope.cos + tr0), tab8(p.rope.sin + tr0));
+          if (!ok) a = bb = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
+          uint16_t* dst = const_cast<uint16_t*>(p.kc) + (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 +
+                          (int64_t)h * p.ks2 + d;
+          *reinterpret_cast<u32x4*>(dst) = a;
+          *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
+        } else if (tensor == 0)
           *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.kc) + (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 +
                                     (int64_t)h * p.ks2 + d) =
               *reinterpret_cast<const u32x4*>(p.kn + row * p.kns0 + (int64_t)h * p.kns1 + d);

@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "cie_flash_fwd_rope",
     "cie_paged_fwd_rope",
     "cie_paged_fwd_append",
+    "cie_paged_fwd_append_rope",
     "cie_kv_append_rope",
     "cie_int8_matmul_workspace_bytes",
     "cie_int8_matmul",
@@ -90,6 +91,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                                          _i, _i, _i, _i, _i, _i, _i, _i, _i,
                                          ctypes.c_float, _i, _i, _vp]
     lib.cie_paged_fwd_append.restype = _i
+    lib.cie_paged_fwd_append_rope.argtypes = lib.cie_paged_fwd_append.argtypes[:-1] + [_vp, _vp, _i, _vp]
+    lib.cie_paged_fwd_append_rope.restype = _i
     lib.cie_kv_append_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                        _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i64p, _vp]
     lib.cie_kv_append_rope.restype = _i

@@ -207,13 +207,14 @@ def paged_attention(
     (B, Hq, Lq, D) tensor to write, as in :func:`flash_attention`.
 
     ``new_kv``: (k_new, v_new), each (B * Lq, Hk, D) with row b * Lq + i =
-    new token i of sequence b, already rotated, not yet in the pool. The
-    append happens in the same launch pair (``cie_paged_fwd_append``):
-    attention reads those rows directly and writes them into the pool at
-    positions ``context_lens[b] - Lq + i``, so the pool and the result equal
+    new token i of sequence b, not yet in the pool. The append happens in the
+    same launch pair (``cie_paged_fwd_append``): attention reads those rows
+    directly and writes them into the pool at positions
+    ``context_lens[b] - Lq + i``, so the pool and the result equal
     ``kv_append`` followed by ``paged_attention`` bit for bit. Every context
-    must count its Lq new tokens (a shorter one gives NaN rows). Not
-    combined with ``rope``.
+    must count its Lq new tokens (a shorter one gives NaN rows). With
+    ``rope`` k_new is un-rotated too and is rotated at those positions, as
+    ``kv_append(rope=)`` would (``cie_paged_fwd_append_rope``).
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_tables", block_tables), ("context_lens", context_lens)):
@@ -239,8 +240,6 @@ def paged_attention(
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if new_kv is not None:
-        if rope is not None:
-            raise ValueError("paged_attention: new_kv takes K already rotated; rope cannot be combined with it")
         k_new, v_new = new_kv
         for name, t in (("k_new", k_new), ("v_new", v_new)):
             if not t.is_cuda or t.device != q.device:
@@ -271,11 +270,14 @@ def paged_attention(
             float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype])
     with torch.cuda.device(q.device):
         if new_kv is not None:
-            rc = lib.cie_paged_fwd_append(q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(),
-                                          v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(), out.data_ptr(),
-                                          workspace.data_ptr(), ws_have, _lib.strides(q), _lib.strides3(k_new),
-                                          _lib.strides3(v_new), _lib.strides(k_cache), _lib.strides(v_cache),
-                                          _lib.strides(out), *args[12:], stream)
+            fargs = (q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                     bt.data_ptr(), lens.data_ptr(), out.data_ptr(), workspace.data_ptr(), ws_have,
+                     _lib.strides(q), _lib.strides3(k_new), _lib.strides3(v_new), _lib.strides(k_cache),
+                     _lib.strides(v_cache), _lib.strides(out), *args[12:])
+            if rope is None:
+                rc = lib.cie_paged_fwd_append(*fargs, stream)
+            else:
+                rc = lib.cie_paged_fwd_append_rope(*fargs, *rope_args(rope, D, q.device), stream)
         elif rope is None:
             rc = lib.cie_paged_fwd(*args, stream)
         else:

@@ -48,9 +48,9 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
     holds the step's device metadata. Returns (B, L, Hq * D).
 
     With ``fuse_append`` (default) a step whose new tokens are the newest of
-    every sequence and whose K is already rotated (``rope`` None) appends
-    inside the paged attention launch pair (``paged_attention(new_kv=...)``),
-    bit-identical to ``append_step`` followed by ``paged_attention``."""
+    every sequence appends inside the paged attention launch pair
+    (``paged_attention(new_kv=..., rope=rope)``), bit-identical to
+    ``append_step`` followed by ``paged_attention``."""
     B, Hq, L, D = q.shape
     if step.context_lens.shape[0] != B or k.shape[0] != B or v.shape[0] != B or step.num_new != L:
         raise ValueError(f"step of {step.context_lens.shape[0]} sequences x {step.num_new} tokens "
@@ -76,11 +76,12 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
             cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope, k_out=k_rot)
             flash_attention(q, k_rot.view(B, L, Hk, D).transpose(1, 2), v, causal=True, scale=scale, rope=rope,
                             out=out)  # positions 0..L-1
-    elif (Hq // Hk) * L <= _PAGED_MAX_ROWS and rope is None and fuse_append and step.aligned:
+    elif (Hq // Hk) * L <= _PAGED_MAX_ROWS and fuse_append and step.aligned:
         cache._validate(k_rows)
         cache._validate(v_rows)
         paged_attention(q, cache.k[layer_idx], cache.v[layer_idx], step.block_tables, step.context_lens,
-                        causal=True, scale=scale, max_context=step.max_context, out=out, new_kv=(k_rows, v_rows))
+                        causal=True, scale=scale, max_context=step.max_context, rope=rope, out=out,
+                        new_kv=(k_rows, v_rows))
     elif (Hq // Hk) * L <= _PAGED_MAX_ROWS:
         cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope)
         q_rope = rope

@@ -228,7 +228,8 @@ int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
  * A context shorter than Lq is invalid here (NaN output, nothing written);
  * a token whose block id is out of range is not written (its sequence's
  * output is NaN, as in cie_paged_fwd). K must already be rotated (no RoPE
- * is applied to it). Same workspace as cie_paged_fwd.
+ * is applied to it; cie_paged_fwd_append_rope rotates it). Same workspace as
+ * cie_paged_fwd.
  * Reference: engine/model/block.py:57-71 (append, then gather + attend).
  */
 int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
@@ -241,6 +242,27 @@ int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
                          int num_blocks, int block_size, int max_blocks_per_seq,
                          int max_context, float scale, int causal, int dtype,
                          void* stream);
+
+/*
+ * cie_paged_fwd_append with RoPE: k_new and q are un-rotated; new token i of
+ * sequence b is rotated at position context_lens[b] - Lq + i, K as it is
+ * used and as it is written into the pool, q as it is loaded. Pool and
+ * output are bit-identical to cie_kv_append_rope (start = context_lens[b] -
+ * Lq) followed by cie_paged_fwd_rope. A position outside [0, rope_rows)
+ * gives NaN rows.
+ * Reference: engine/model/block.py:53-54 (RoPE) and :57-71.
+ */
+int cie_paged_fwd_append_rope(const void* q, const void* k_new, const void* v_new,
+                              const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              void* o, void* workspace, size_t workspace_bytes,
+                              const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
+                              const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,
+                              int B, int Hq, int Hk, int Lq, int D,
+                              int num_blocks, int block_size, int max_blocks_per_seq,
+                              int max_context, float scale, int causal, int dtype,
+                              const float* rope_cos, const float* rope_sin, int rope_rows,
+                              void* stream);
 
 /*
  * cie_kv_append with RoPE fused into the write of K: k_new holds the

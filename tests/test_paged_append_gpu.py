@@ -4,7 +4,10 @@ cie_kv_append of the new tokens (the reference's append loop,
 engine/cache/kv_cache.py:128-136) followed by cie_paged_fwd (the reference's
 gather + attend, engine/model/block.py:57-71). The bar is bit-exactness of
 both pools and of the output: the fused launch reads the same values and
-runs the same arithmetic; the oracle check confirms the result too."""
+runs the same arithmetic; the oracle check confirms the result too. With
+RoPE the reference rotates q and k first (engine/model/block.py:53-54); the
+fused pair rotates the new K rows itself, bit-identical to the rotating
+append."""
 
 from __future__ import annotations
 
@@ -98,13 +101,35 @@ def test_fused_append_invalid_context_and_block_id():
         assert torch.equal(k1[blk], kp[blk]) and torch.equal(v1[blk], vp[blk]), blk
 
 
-def test_fused_append_rejects_rope_and_bad_shapes():
+@pytest.mark.parametrize("Lq", [1, 5])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_append_with_rope_equals_rotating_append_then_attend(Lq, D, dtype):
+    """q and k_new un-rotated: the fused pair rotates the new K rows in LDS
+    and on their way into the pool, bit-identical to kv_append(rope=) then
+    paged_attention(rope=)."""
+    from engine.model.rope import RotaryEmbedding
+
+    emb = RotaryEmbedding(D, 8192).to(DEV)
+    lens = [Lq, 40 + Lq, 700, 2049, 4096, 33]
+    q, kp, vp, bt, lt = make_paged(lens, Lq, D, dtype, 16, Hq=8, Hk=2, seed=D + Lq, vscale=0.5)
+    k_new, v_new = _new_rows(len(lens), Lq, 2, D, dtype, seed=21 + Lq)
+    kd, vd = kp.to(DEV), vp.to(DEV)
+    B = len(lens)
+    cu = torch.arange(0, B * Lq + 1, Lq, dtype=torch.int32, device=DEV)
+    kv_append(k_new.to(DEV), v_new.to(DEV), kd, vd, bt.to(DEV), cu, (lt - Lq).to(DEV), max_new=Lq, rope=emb.tables)
+    o2 = paged_attention(q.to(DEV), kd, vd, bt.to(DEV), lt.to(DEV), causal=True, rope=emb.tables).cpu()
+    o1, k1, v1 = _fused(q, kp, vp, bt, lt, k_new, v_new, rope=emb.tables)
+    assert torch.equal(k1, kd.cpu()) and torch.equal(v1, vd.cpu()), "pool after the rotating fused append differs"
+    assert torch.equal(o1, o2), (o1.float() - o2.float()).abs().max().item()
+
+
+def test_fused_append_rejects_bad_shapes():
     q, kp, vp, bt, lt = make_paged([40], 1, 64, torch.float16, 16)
     k_new, v_new = _new_rows(1, 1, 2, 64, torch.float16, seed=1)
-    cos = torch.ones(64, 32, device=DEV)
-    with pytest.raises(ValueError):
-        paged_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV), lt.to(DEV),
-                        new_kv=(k_new.to(DEV), v_new.to(DEV)), rope=(cos, cos))
     with pytest.raises(ValueError):
         paged_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV), lt.to(DEV),
                         new_kv=(k_new[:, :1].to(DEV), v_new.to(DEV)))
+    with pytest.raises(ValueError):
+        paged_attention(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV), lt.to(DEV),
+                        new_kv=(k_new.to(DEV), v_new.to(DEV).float()))
