@@ -139,7 +139,9 @@ __device__ __forceinline__ void store_row(uint16_t* row, const f32x16* acc, floa
   }
 }
 
-template <int DTYPE, int D>
+// APPEND: the fused-append variant (p.kn set), a separate instantiation so
+// the plain kernel carries none of its registers or branches.
+template <int DTYPE, int D, bool APPEND>
 __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const PagedParams p) {
   using C = PagedCfg<D>;
   using E = Elt<DTYPE>;
@@ -271,7 +273,8 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   // (P % NCH) ^ row_swizzle(token) of the token's group row.
   int ltok[C::DPW];
   int64_t goffk[C::DPW], goffv[C::DPW];
-  int64_t gnk[C::DPW], gnv[C::DPW];  // the same chunk in a new-token row (fused append)
+  constexpr int NA = APPEND ? C::DPW : 1;
+  int64_t gnk[NA], gnv[NA];  // the same chunk in a new-token row (fused append)
 #pragma unroll
   for (int x = 0; x < C::DPW; ++x) {
     const int P = 64 * (hh * C::DPW + x) + lane;
@@ -280,8 +283,10 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const int hd = c / C::S, dc = c % C::S;
     ltok[x] = tk;
     goffk[x] = (int64_t)(gh * p.Hg + hd) * p.ks2 + 8 * dc;
-    gnk[x] = (int64_t)(gh * p.Hg + hd) * p.kns1 + 8 * dc;
-    gnv[x] = (int64_t)(gh * p.Hg + hd) * p.vns1 + 8 * dc;
+    if constexpr (APPEND) {
+      gnk[x] = (int64_t)(gh * p.Hg + hd) * p.kns1 + 8 * dc;
+      gnv[x] = (int64_t)(gh * p.Hg + hd) * p.vns1 + 8 * dc;
+    }
     goffv[x] = (int64_t)(gh * p.Hg + hd) * p.vs2 + 8 * dc;
   }
   // Fragment reads: K row l32 (chunk 2 kk + hl of head hh), V^T rows.
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const int tbase = kPagedTile * (i_ttlo + k - i_base);
     const uint32_t st = ring_lds + 2u * (uint32_t)(i_stage * STAGE_EL) + 1024u * (uint32_t)(hh * C::DPW);
     i_stage = i_stage + 1 == NST ? 0 : i_stage + 1;
-    if (p.kn && tbase + kPagedTile > i_ctx - p.Lq) {
+    if (APPEND && tbase + kPagedTile > i_ctx - p.Lq) {
       // a tile holding new tokens: those rows come from kn / vn, the rest
       // from the pool (per-lane addresses)
 #pragma unroll
@@ -334,8 +339,8 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         const uint16_t *sk, *sv;
         if (tk >= i_ctx - p.Lq) {
           const int64_t row = (int64_t)i_b * p.Lq + (tk - (i_ctx - p.Lq));
-          sk = p.kn + row * p.kns0 + gnk[x];
-          sv = p.vn + row * p.vns0 + gnv[x];
+          sk = p.kn + row * p.kns0 + gnk[APPEND ? x : 0];
+          sv = p.vn + row * p.vns0 + gnv[APPEND ? x : 0];
         } else {
           const int blk = (int)fdiv((uint32_t)tk, p.bsdiv);
           const int off = tk - blk * p.block_size;
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const uint16_t* vst = kst + TILE_EL;
     c_stage = c_stage + 1 == NST ? 0 : c_stage + 1;
     const int t0 = kPagedTile * (c_ttlo + n - c_base);
-    if (p.kn && p.rope.cos && t0 + kPagedTile > c_ctx - p.Lq) {
+    if (APPEND && p.rope.cos && t0 + kPagedTile > c_ctx - p.Lq) {
       // fused append with RoPE: the new K rows of this tile arrived
       // unrotated from kn; rotate them in LDS at their positions (pairs of
       // 16-byte chunks j, j + D/16 of each head, found through the row
@@ -582,7 +587,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   // head group's rows of each (16-byte chunks over the whole workgroup).
   // Nothing in this launch reads those pool rows (the tiles holding them
   // took the rows from kn / vn), so no ordering is needed.
-  if (p.kn) {
+  if (APPEND) {
     const int cpr = p.Hg * (D / 8);  // chunks of one tensor per token row of the head group
     const bool rot = p.rope.cos != nullptr;
     for (int e = 0; e < ne; ++e) {
@@ -799,10 +804,15 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
 
 template <int DTYPE, int D>
 static hipError_t launch_paged_t(const PagedParams& p, size_t lds, hipStream_t stream) {
-  const hipError_t attr = set_dynamic_lds(reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D>), kPagedLdsBudget);
+  const void* fn = p.kn ? reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D, true>)
+                        : reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D, false>);
+  const hipError_t attr = set_dynamic_lds(fn, kPagedLdsBudget);
   if (attr != hipSuccess) return attr;
   const int64_t n_wg = (int64_t)p.NG * p.Wg;
-  hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
+  if (p.kn)
+    hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D, true>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
+  else
+    hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D, false>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t threads = (int64_t)p.B * p.NG * p.NWV * p.Rt * (D / 4) * kMergeLanes;
