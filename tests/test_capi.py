@@ -114,6 +114,38 @@ def test_paged_rejects_bad_arguments(over, code):
     assert _lib.last_error()
 
 
+def _paged_append(rope=False, **over):
+    args = dict(q=FAKE, kn=FAKE, vn=FAKE, kc=FAKE, vc=FAKE, bt=FAKE, lens=FAKE, o=FAKE, ws=FAKE, ws_bytes=1 << 30,
+                qs=_st(2048, 64, 64, 1), kns=_st(512, 64, 1, 0), vns=_st(512, 64, 1, 0),
+                ks=_st(8192, 512, 64, 1), vs=_st(8192, 512, 64, 1),
+                os_=_st(2048, 64, 64, 1), B=4, Hq=32, Hk=8, Lq=1, D=64, nb=100, bs=16, mb=25, mc=0,
+                scale=0.125, causal=1, dtype=0)
+    args.update(over)
+    a = args
+    head = (a["q"], a["kn"], a["vn"], a["kc"], a["vc"], a["bt"], a["lens"], a["o"], a["ws"], a["ws_bytes"],
+            a["qs"], a["kns"], a["vns"], a["ks"], a["vs"], a["os_"], a["B"], a["Hq"], a["Hk"], a["Lq"], a["D"],
+            a["nb"], a["bs"], a["mb"], a["mc"], a["scale"], a["causal"], a["dtype"])
+    lib = _lib.load()
+    if rope:
+        return lib.cie_paged_fwd_append_rope(*head, FAKE, FAKE, 4096, None)
+    return lib.cie_paged_fwd_append(*head, None)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("over,code", [
+    (dict(kn=0), _lib.CIE_EINVAL),
+    (dict(vn=0), _lib.CIE_EINVAL),
+    (dict(kn=FAKE + 8), _lib.CIE_EINVAL),                  # not 16-byte aligned
+    (dict(kns=_st(500, 64, 1, 0)), _lib.CIE_EINVAL),       # token stride not a multiple of 8
+    (dict(D=24), _lib.CIE_EHEADDIM),
+    (dict(ws_bytes=16), _lib.CIE_EWORKSPACE),
+])
+def test_paged_append_rejects_bad_arguments(rope, over, code):
+    """The fused append entries validate before any launch (no GPU needed)."""
+    assert _paged_append(rope=rope, **over) == code
+    assert _lib.last_error()
+
+
 def test_paged_workspace_size():
     lib = _lib.load()
     # counters for every (head group, sequence) plus partial slots
