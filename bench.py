@@ -61,6 +61,10 @@ def parse():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only a 256 MiB copy (counter calibration), the prefill kernel and the "
                          "paged decode / verify pairs, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+    ap.add_argument("--probe", default="",
+                    help="comma-separated workloads (prefill_s2048, prefill_s16384, decode_b32, verify_b8): "
+                         "run only the 256 MiB calibration copy and three launches of each, for rocprofv3 "
+                         "--pmc counter runs")
     return ap.parse_args()
 
 
@@ -80,7 +84,9 @@ def traffic_from_summary():
     return None
 
 
-def traffic_probe():
+def traffic_probe(names=("prefill_s2048", "decode_b32", "verify_b8")):
+    """The calibration copy, then three launches of each named workload
+    (paged ones on distinct pool copies): short runs for counter passes."""
     import torch
 
     from benchmarks import workloads
@@ -90,18 +96,17 @@ def traffic_probe():
     y = torch.empty_like(x)
     for _ in range(3):
         y.copy_(x)  # 256 MiB read + 256 MiB written per dispatch
-    fl = FlashLaunch(workloads.prefill_s2048(), dev)
-    for _ in range(3):
-        fl()
     torch.cuda.synchronize()
-    del fl
-    for name in ("decode_b32", "verify_b8"):  # the paged pair, three launches each on distinct pool copies
-        pl = PagedLaunch(workloads.WORKLOADS[name](), dev)
+    del x, y
+    for name in names:
+        case = workloads.WORKLOADS[name]()
+        launch = FlashLaunch(case, dev) if name.startswith("prefill") else PagedLaunch(case, dev)
         for i in range(3):
-            pl(i)
+            launch(i)
         torch.cuda.synchronize()
-        del pl
-    print("traffic probe done", flush=True)
+        del launch
+        torch.cuda.empty_cache()
+        print(f"probe {name} done", flush=True)
 
 
 class FlashLaunch:
@@ -236,7 +241,7 @@ class RopeLaunch:
         x = torch.randn(B, H, L, D).half().to(dev)
         self.bufs = [x.clone() for _ in range(self.copies)]
         self._st = _lib.strides(x)
-        self.tail = (self._st, self._st, None, 0, self.cos.data_ptr(), self.sin.data_ptr(), 4096, None,
+        self.tail = (self._st, self._st, None, 0, self.cos.data_ptr(), self.sin.data_ptr(), 4096, 2, None,
                      B, H, L, D, 0)
         self.dev = dev
         self.bytes = 2 * per  # read once, written once (the fp32 tables: 0.5 MiB more, from L2)
@@ -515,6 +520,9 @@ def main():
     args = parse()
     if args.traffic_probe:
         traffic_probe()
+        return
+    if args.probe:
+        traffic_probe(tuple(n for n in args.probe.split(",") if n))
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))

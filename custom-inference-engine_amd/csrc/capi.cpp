@@ -93,11 +93,14 @@ void set_scale(float scale, float* c, uint32_t* q_sign) {
   *c = std::max(std::fabs(scale) * cie::kLog2e, 1e-30f);
 }
 
-// cos / sin: fp32 (rows, D/2) row-major tables, as RotaryEmbedding holds them.
-int check_rope(const float* cos, const float* sin, int rows) {
+// cos / sin: (rows, D/2) row-major tables of element type dt (fp16, bf16 or
+// fp32), as RotaryEmbedding holds them before or after the engine's cast.
+int check_rope(const void* cos, const void* sin, int rows, int dt) {
   if (!cos || !sin) return fail(CIE_EINVAL, "rope tables: NULL pointer");
   if (!aligned16(cos) || !aligned16(sin)) return fail(CIE_EINVAL, "rope tables: pointer is not 16-byte aligned");
   if (rows < 1) return fail(CIE_EINVAL, "rope tables need at least one row, got %d", rows);
+  if (dt != CIE_TABLE_F16 && dt != CIE_TABLE_BF16 && dt != CIE_TABLE_F32)
+    return fail(CIE_EDTYPE, "unsupported rope table dtype code %d (f16 = 0, bf16 = 1, f32 = 2)", dt);
   return CIE_OK;
 }
 
@@ -173,7 +176,7 @@ int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
                   int B, int Hq, int Hk, int Lq, int Lk, int D,
                   float scale, int causal, int dtype, void* stream) {
   return flash_impl(q, k, v, o, q_stride, k_stride, v_stride, o_stride, B, Hq, Hk, Lq, Lk, D, scale, causal,
-                    dtype, stream, cie::RopeTables{nullptr, nullptr, 0}, nullptr);
+                    dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0}, nullptr);
 }
 
 int cie_flash_fwd_rope(const void* q, const void* k, const void* v, void* o,
@@ -181,11 +184,11 @@ int cie_flash_fwd_rope(const void* q, const void* k, const void* v, void* o,
                        const int64_t* v_stride, const int64_t* o_stride,
                        int B, int Hq, int Hk, int Lq, int Lk, int D,
                        float scale, int causal, int dtype,
-                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                        const int32_t* q_pos0, void* stream) {
-  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows, rope_dtype));
   return flash_impl(q, k, v, o, q_stride, k_stride, v_stride, o_stride, B, Hq, Hk, Lq, Lk, D, scale, causal,
-                    dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, q_pos0);
+                    dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows, rope_dtype}, q_pos0);
 }
 
 // Largest valid context length: the table bound, tightened by the caller's hint.
@@ -322,7 +325,7 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
                   void* stream) {
   return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
                     kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
-                    max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0});
+                    max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0});
 }
 
 int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
@@ -333,16 +336,17 @@ int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
                        int B, int Hq, int Hk, int Lq, int D,
                        int num_blocks, int block_size, int max_blocks_per_seq,
                        int max_context, float scale, int causal, int dtype,
-                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                        void* stream) {
-  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows, rope_dtype));
   return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
                     kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
-                    max_context, scale, causal, dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows});
+                    max_context, scale, causal, dtype, stream,
+                    cie::RopeTables{rope_cos, rope_sin, rope_rows, rope_dtype});
 }
 
 int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
-                         const void* k_cache, const void* v_cache,
+                         void* k_cache, void* v_cache,
                          const int32_t* block_tables, const int32_t* context_lens,
                          void* o, void* workspace, size_t workspace_bytes,
                          const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
@@ -354,12 +358,12 @@ int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
   if (!k_new || !v_new) return fail(CIE_EINVAL, "k_new / v_new: NULL pointer");
   return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
                     kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
-                    max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0}, k_new, v_new,
+                    max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0}, k_new, v_new,
                     kn_stride, vn_stride);
 }
 
 int cie_paged_fwd_append_rope(const void* q, const void* k_new, const void* v_new,
-                              const void* k_cache, const void* v_cache,
+                              void* k_cache, void* v_cache,
                               const int32_t* block_tables, const int32_t* context_lens,
                               void* o, void* workspace, size_t workspace_bytes,
                               const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
@@ -367,14 +371,14 @@ int cie_paged_fwd_append_rope(const void* q, const void* k_new, const void* v_ne
                               int B, int Hq, int Hk, int Lq, int D,
                               int num_blocks, int block_size, int max_blocks_per_seq,
                               int max_context, float scale, int causal, int dtype,
-                              const float* rope_cos, const float* rope_sin, int rope_rows,
+                              const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                               void* stream) {
   if (!k_new || !v_new) return fail(CIE_EINVAL, "k_new / v_new: NULL pointer");
-  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows, rope_dtype));
   return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
                     kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
-                    max_context, scale, causal, dtype, stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, k_new,
-                    v_new, kn_stride, vn_stride);
+                    max_context, scale, causal, dtype, stream,
+                    cie::RopeTables{rope_cos, rope_sin, rope_rows, rope_dtype}, k_new, v_new, kn_stride, vn_stride);
 }
 
 }  // extern "C"
@@ -462,7 +466,7 @@ int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
                   int num_blocks, int block_size, int max_blocks_per_seq, int dtype, void* stream) {
   return append_impl(k_new, v_new, k_cache, v_cache, new_stride, v_new_stride, kc_stride, vc_stride, block_tables,
                      cu_new, start, status, B, T, max_new, Hk, D, num_blocks, block_size, max_blocks_per_seq, dtype,
-                     stream, cie::RopeTables{nullptr, nullptr, 0}, nullptr, nullptr);
+                     stream, cie::RopeTables{nullptr, nullptr, 0, 0}, nullptr, nullptr);
 }
 
 int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
@@ -471,16 +475,16 @@ int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void
                        const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
                        uint32_t* status, int B, int T, int max_new, int Hk, int D,
                        int num_blocks, int block_size, int max_blocks_per_seq, int dtype,
-                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                        void* k_out, const int64_t* k_out_stride, void* stream) {
-  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows, rope_dtype));
   return append_impl(k_new, v_new, k_cache, v_cache, new_stride, v_new_stride, kc_stride, vc_stride, block_tables,
                      cu_new, start, status, B, T, max_new, Hk, D, num_blocks, block_size, max_blocks_per_seq, dtype,
-                     stream, cie::RopeTables{rope_cos, rope_sin, rope_rows}, k_out, k_out_stride);
+                     stream, cie::RopeTables{rope_cos, rope_sin, rope_rows, rope_dtype}, k_out, k_out_stride);
 }
 
 size_t cie_int8_matmul_workspace_bytes(int M, int N, int K) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
   return cie::int8_gemm_geometry(M, N, K).workspace_bytes;
 }
 
@@ -493,7 +497,6 @@ int cie_int8_matmul(const void* x, const int8_t* w, const void* scales, const vo
   if (scale_dtype < 0 || scale_dtype > 2)
     return fail(CIE_EDTYPE, "unsupported scale dtype code %d (f16 = 0, bf16 = 1, f32 = 2)", scale_dtype);
   if (M < 0 || N < 0 || K < 0) return fail(CIE_EINVAL, "negative size (M=%d, N=%d, K=%d)", M, N, K);
-  if (K % 64) return fail(CIE_EINVAL, "in_features K=%d must be a multiple of 64", K);
   if ((int64_t)M * N == 0) {
     g_err.clear();
     return CIE_OK;
@@ -538,7 +541,7 @@ int cie_int8_matmul(const void* x, const int8_t* w, const void* scales, const vo
 
 int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int64_t* out_stride,
                    const int32_t* positions, int64_t pos_batch_stride,
-                   const float* rope_cos, const float* rope_sin, int rope_rows,
+                   const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                    uint32_t* status, int B, int H, int L, int D, int dtype, void* stream) {
   if (dtype != CIE_DTYPE_F16 && dtype != CIE_DTYPE_BF16)
     return fail(CIE_EDTYPE, "unsupported dtype code %d (f16 = 0, bf16 = 1)", dtype);
@@ -546,7 +549,7 @@ int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int6
   if (B < 0 || H < 0 || L < 0 || pos_batch_stride < 0)
     return fail(CIE_EINVAL, "invalid sizes (B=%d, H=%d, L=%d, pos_batch_stride=%lld)", B, H, L,
                 (long long)pos_batch_stride);
-  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows));
+  CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows, rope_dtype));
   // eight heads per thread where that still gives 512 workgroups (4 x 32 x
   // 2048 x 64: 19.0 -> 16.8 us); one head per thread for smaller launches,
   // where fewer, longer threads were slower (a 32-sequence decode step's q:
@@ -570,7 +573,7 @@ int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int6
   p.os0 = out_stride[0]; p.os1 = out_stride[1]; p.os2 = out_stride[2];
   p.pos = positions;
   p.pos_bs = pos_batch_stride;
-  p.tab = cie::RopeTables{rope_cos, rope_sin, rope_rows};
+  p.tab = cie::RopeTables{rope_cos, rope_sin, rope_rows, rope_dtype};
   p.status = status;
   p.B = B; p.H = H; p.L = L;
   p.HG = hg;

@@ -140,8 +140,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 #pragma unroll
   for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
   if (p.rope.cos)  // RoPE fused into the load: row qi at position q_pos0[b] + qi
-    rope_q_lane<DTYPE, D>(qf, p.rope.cos, p.rope.sin, p.rope.rows, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq,
-                          hl);
+    rope_q_lane<DTYPE, D>(qf, p.rope, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq, hl);
   const float c = p.scale_log2;
   {
     const float cq = p.q_sign ? -c : c;

@@ -29,6 +29,13 @@
 // MFMA kernel (both one launch, no workspace; below), above that the tiled
 // kernel described here.
 //
+// Any K. The reference masks the K tail of its last tile
+// (kernels/int8_matmul.py:43-50). Here each kernel's main loop covers the
+// largest prefix of K its step divides (64 for the tiled kernel, 32 for the
+// streaming one, 16 for the dot kernel) and never reads past it; the
+// remaining k < 64 terms of every output are added in the epilogue, in fp32
+// with exact products and in ascending k, before the scale is applied.
+//
 // Split K. When the (n, m) tiles alone cannot occupy the GPU, the K steps
 // are cut into `splits` contiguous ranges; each
 // workgroup writes its fp32 partial tile to the workspace in lane order
@@ -151,6 +158,18 @@ __device__ __forceinline__ void store4(const I8GemmParams& p, int m, int n, u32x
     const uint16_t h[4] = {(uint16_t)pk[0], (uint16_t)(pk[0] >> 16), (uint16_t)pk[1], (uint16_t)(pk[1] >> 16)};
     for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = h[e];
   }
+}
+
+// sum over k in [k0, K) of x[m][k] * w[n][k] (products exact in fp32), k
+// ascending, with m, n clamped into the tensors (rows past M / N are never
+// stored). The K tail the vector main loops leave.
+template <int DTYPE>
+__device__ __forceinline__ float tail_dot(const I8GemmParams& p, int m, int n, int k0) {
+  const uint16_t* xr = p.x + (int64_t)min(m, p.M - 1) * p.xs;
+  const int8_t* wr = p.w + (int64_t)min(n, p.N - 1) * p.wsr;
+  float a = 0.f;
+  for (int k = k0; k < p.K; ++k) a = fmaf(elt_to_f32<DTYPE>(xr[k]), (float)wr[k], a);
+  return a;
 }
 
 // vm_wait for the copies of `ahead` k steps issued after the one needed (uniform `ahead`)
@@ -281,6 +300,39 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
 
   // C[i][j] of a 32x32 tile: lane j + 32 * ((i / 4) % 2), element (i / 8) * 4 + i % 4;
   // here i = weight row (n), j = activation row (m)
+  const int k_main = p.ksteps * kI8BK;  // k of the MFMA steps; the last split adds the tail
+  if (k_main < p.K && split == p.splits - 1) {
+    // this lane's MT activation rows and 16 weight rows, clamped into the
+    // tensors (rows past M / N are never stored); each tail k loads every
+    // row's element once
+    const uint16_t* xr[MT];
+    const int8_t* wr[16];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xr[mt] = p.x + (int64_t)min(m0 + mt * 32 + r32, p.M - 1) * p.xs;
+#pragma unroll
+    for (int el = 0; el < 16; ++el)
+      wr[el] = p.w + (int64_t)min(n0 + w * 32 + 8 * (el >> 2) + 4 * hk + (el & 3), p.N - 1) * p.wsr;
+    float ta[MT][16];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int el = 0; el < 16; ++el) ta[mt][el] = 0.f;
+    for (int k = k_main; k < p.K; ++k) {
+      float xv[MT], wv[16];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xv[mt] = elt_to_f32<DTYPE>(xr[mt][k]);
+#pragma unroll
+      for (int el = 0; el < 16; ++el) wv[el] = (float)wr[el][k];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int el = 0; el < 16; ++el) ta[mt][el] = fmaf(xv[mt], wv[el], ta[mt][el]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int el = 0; el < 16; ++el) acc[mt][el] += ta[mt][el];
+  }
   if (p.splits == 1) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -519,6 +571,10 @@ __global__ __launch_bounds__(256) void int8_gemv_kernel(const I8GemmParams p) {
       a[3] += v[3];
     }
     const int n = n0 + 4 * (lane >> 4);
+    if (32 * G < p.K) {  // the K tail past the last whole 32-k group
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] += tail_dot<DTYPE>(p, 16 * w + (lane & 15), n + e, 32 * G);
+    }
     store4<DTYPE>(p, 16 * w + (lane & 15), n, finish4<DTYPE>(a, p, n));
   }
 }
@@ -557,8 +613,9 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
   constexpr int PERC = kDotRows + 2 * MC;  // loads per chunk
   const int lane = threadIdx.x;
   const int n0 = blockIdx.x * kDotRows;
-  const int nch = (p.K + 1023) >> 10;
-  const bool tail = (p.K & 1023) != 0;
+  const int K16 = p.K & ~15;  // k of the 16-element lane chunks; the rest is added at the end
+  const int nch = (K16 + 1023) >> 10;
+  const bool tail = (K16 & 1023) != 0;
   // rows past N / M are clamped to the last one (loaded, never stored)
   const int8_t* wrow[kDotRows];
 #pragma unroll
@@ -568,10 +625,10 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
   for (int m = 0; m < MC; ++m) xrow[m] = p.x + (int64_t)min(m, p.M - 1) * p.xs;
 
   u32x4 wq[kDotDepth][kDotRows], xq[kDotDepth][MC][2];
-  // chunk c into ring slot s; lanes past K (last chunk) read its last 16 k, zeroed before use
+  // chunk c into ring slot s; lanes past K16 (last chunk) read its last 16 k, zeroed before use
   auto issue = [&](auto S, int c) CIE_GV_INLINE {
     constexpr int s = decltype(S)::value;
-    const int k = min(1024 * c + 16 * lane, p.K - 16);
+    const int k = min(1024 * c + 16 * lane, K16 - 16);
 #pragma unroll
     for (int r = 0; r < kDotRows; ++r) wq[s][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + k));
 #pragma unroll
@@ -595,7 +652,7 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
       const int c = c0 + s;
       if (c < nch) {  // wave-uniform
         wait_steps_ahead<PERC, kDotDepth - 1>(min(kDotDepth - 1, nch - 1 - c));
-        const bool kin = !(tail && c == nch - 1) || 1024 * c + 16 * lane < p.K;
+        const bool kin = !(tail && c == nch - 1) || 1024 * c + 16 * lane < K16;
 #pragma unroll
         for (int r = 0; r < kDotRows; ++r) {
           u32x4 a0, a1;
@@ -628,6 +685,7 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
   const int r = lane / MC, m = lane - (lane / MC) * MC;
   if (lane < kDotRows * MC && m < p.M && n0 + r < p.N) {
     const int n = n0 + r;
+    if (K16 < p.K) out += tail_dot<DTYPE>(p, m, n, K16);
     float t = out * load_scale(p.scales, n, p.scale_dtype);
     if (p.bias) {  // the reference adds the bias to the rounded product, in the output dtype
       const uint32_t rr = Elt<DTYPE>::pack2(t, 0.f);

@@ -10,12 +10,15 @@
 
 namespace cie {
 
-// Rotary tables of the kernels that apply RoPE: cos, sin fp32 (rows, D/2),
-// contiguous. cos == nullptr: no rotation.
+// Rotary tables of the kernels that apply RoPE: cos, sin of shape (rows, D/2),
+// contiguous, elements of type dt (kTabF16, kTabBF16 or kTabF32).
+// cos == nullptr: no rotation.
+constexpr int kTabF16 = 0, kTabBF16 = 1, kTabF32 = 2;
 struct RopeTables {
-  const float* cos;
-  const float* sin;
+  const void* cos;
+  const void* sin;
   int rows;
+  int dt;
 };
 
 // Dense attention. Strides are in elements; head_dim stride is 1.

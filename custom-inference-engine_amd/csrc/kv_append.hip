@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
 
 // With RoPE on K (rope/rope.hpp restates kernels/ref/rope_apply_ref.py:46-53):
 // one thread moves the chunk pair (j, j + D/16) of one head of one token, K
-// rotated at position start[b] + i through the fp32 tables, V copied, both
+// rotated at position start[b] + i through the tables, V copied, both
 // pairs written to the pool and the rotated K optionally also to the dense
 // k_out rows (what prefill attention over the new tokens reads).
 constexpr int kRopeUnroll = 2;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(const AppendParams 
   uint32_t bad = 0;
   for (uint32_t c0 = blockIdx.x * 256u + threadIdx.x; c0 < total; c0 += kRopeUnroll * stride) {
     u32x4 klo[kRopeUnroll], khi[kRopeUnroll], vlo[kRopeUnroll], vhi[kRopeUnroll];
-    f32x8 cs[kRopeUnroll], sn[kRopeUnroll];
+    RopeChunk cs[kRopeUnroll];
     int64_t dk[kRopeUnroll], dv[kRopeUnroll], dout[kRopeUnroll];
     bool in[kRopeUnroll], ok[kRopeUnroll];
 #pragma unroll
@@ -132,15 +132,14 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(const AppendParams 
       vlo[u] = *reinterpret_cast<const u32x4*>(vs);
       vhi[u] = *reinterpret_cast<const u32x4*>(vs + half);
       const int64_t tr = (rope_ok ? (int64_t)pos : 0) * half + 8 * j;
-      cs[u] = tab8(p.rope.cos + tr);
-      sn[u] = tab8(p.rope.sin + tr);
+      cs[u] = rope_load(p.rope, tr);
       dk[u] = (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 + h * p.ks2 + 8 * j;
       dv[u] = (int64_t)bid * p.vs0 + (int64_t)off * p.vs1 + h * p.vs2 + 8 * j;
       dout[u] = row * p.os0 + h * p.os1 + 8 * j;
     }
 #pragma unroll
     for (int u = 0; u < kRopeUnroll; ++u) {
-      rope8<DTYPE>(klo[u], khi[u], cs[u], sn[u]);
+      rope_apply8<DTYPE>(klo[u], khi[u], cs[u], p.rope.dt);
       if (ok[u]) {
         __builtin_nontemporal_store(klo[u], reinterpret_cast<u32x4*>(p.kc + dk[u]));
         __builtin_nontemporal_store(khi[u], reinterpret_cast<u32x4*>(p.kc + dk[u] + half));

@@ -411,8 +411,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   if (p.rope.cos) {  // RoPE fused into the load: row i at position ctx - Lq + i
 #pragma unroll
     for (int e = 0; e < C::QPRE; ++e)
-      rope_q_lane<DTYPE, D>(qpre[e], p.rope.cos, p.rope.sin, p.rope.rows, (e < ne ? ent[e][1] : 0) - p.Lq + i,
-                            rv && e < ne, hl);
+      rope_q_lane<DTYPE, D>(qpre[e], p.rope, (e < ne ? ent[e][1] : 0) - p.Lq + i, rv && e < ne, hl);
   }
 #pragma unroll
   for (int e = 0; e < C::QPRE; ++e)
@@ -458,7 +457,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
       } else {
 #pragma unroll
         for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + c_b * p.qs0 + 16 * kk + 8 * hl, rv);
-        if (p.rope.cos) rope_q_lane<DTYPE, D>(qf, p.rope.cos, p.rope.sin, p.rope.rows, c_ctx - p.Lq + i, rv, hl);
+        if (p.rope.cos) rope_q_lane<DTYPE, D>(qf, p.rope, c_ctx - p.Lq + i, rv, hl);
 #pragma unroll
         for (int kk = 0; kk < C::KK; ++kk) qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
       }
@@ -494,7 +493,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         u32x4 a = *lo, b = *hi;
         const bool ok = pos < p.rope.rows;
         const int64_t tr0 = (ok ? (int64_t)pos : 0) * (D / 2) + 8 * jj;
-        rope8<DTYPE>(a, b, tab8(p.rope.cos + tr0), tab8(p.rope.sin + tr0));
+        rope_apply8<DTYPE>(a, b, rope_load(p.rope, tr0), p.rope.dt);
         if (!ok) a = b = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
         *lo = a;
         *hi = b;
@@ -601,6 +600,9 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         const int blk = (int)fdiv((uint32_t)pos, p.bsdiv);
         const int bid = sbt[idb + blk - blk_lo];
         if (bid < 0) continue;  // invalid block id: the output is NaN, nothing is written
+        // a position outside the rotary tables: NaN output rows, neither K nor
+        // V written (as the rotating append leaves the pool)
+        if (rot && pos >= p.rope.rows) continue;
         const int off = pos - blk * p.block_size;
         const int h = gh * p.Hg + c / (D / 8), d = 8 * (c % (D / 8));
         const int64_t row = (int64_t)b * p.Lq + (pos - (ctx - p.Lq));
@@ -609,10 +611,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
           if (d >= D / 2) continue;
           const uint16_t* src = p.kn + row * p.kns0 + (int64_t)h * p.kns1 + d;
           u32x4 a = *reinterpret_cast<const u32x4*>(src), bb = *reinterpret_cast<const u32x4*>(src + D / 2);
-          const bool ok = pos < p.rope.rows;
-          const int64_t tr0 = (ok ? (int64_t)pos : 0) * (D / 2) + d;
-          rope8<DTYPE>(a, bb, tab8(p.rope.cos + tr0), tab8(p.rope.sin + tr0));
-          if (!ok) a = bb = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
+          rope_apply8<DTYPE>(a, bb, rope_load(p.rope, (int64_t)pos * (D / 2) + d), p.rope.dt);
           uint16_t* dst = const_cast<uint16_t*>(p.kc) + (int64_t)bid * p.ks0 + (int64_t)off * p.ks1 +
                           (int64_t)h * p.ks2 + d;
           *reinterpret_cast<u32x4*>(dst) = a;

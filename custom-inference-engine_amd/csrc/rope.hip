@@ -5,8 +5,8 @@
 //
 // One thread rotates one chunk pair (x[j*8 .. +8), x[D/2 + j*8 .. +8)) of
 // one position l in each of up to HG heads (HG = kRopeHeads for launches
-// large enough to keep 512 workgroups, else 1): the fp32 cos/sin row chunks
-// of the position (read through L2) are loaded once for all of them, and
+// large enough to keep 512 workgroups, else 1): the cos/sin row chunks of
+// the position (read through L2) are loaded once for all of them, and
 // the thread's 2 * HG row loads are in flight together.
 // Consecutive threads take consecutive chunk pairs of a row, then the next
 // position, so for every head the loads and stores of a wave cover
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
     const bool ok = pos >= 0 && pos < p.tab.rows;
     bad |= !ok;
     const int64_t tr = (ok ? (int64_t)pos : 0) * HALF + 8 * j;
-    const f32x8 c = tab8(p.tab.cos + tr), s = tab8(p.tab.sin + tr);
+    const RopeChunk cs = rope_load(p.tab, tr);
     const uint16_t* x = p.x + (int64_t)b * p.xs0 + (int64_t)h0 * p.xs1 + (int64_t)l * p.xs2 + 8 * j;
     uint16_t* o = p.out + (int64_t)b * p.os0 + (int64_t)h0 * p.os1 + (int64_t)l * p.os2 + 8 * j;
     u32x4 lo[HG], hi[HG];
@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
 #pragma unroll
     for (int e = 0; e < HG; ++e) {
       if (e < nh) {
-        rope8<DTYPE>(lo[e], hi[e], c, s);
+        rope_apply8<DTYPE>(lo[e], hi[e], cs, p.tab.dt);
         if (!ok) lo[e] = hi[e] = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
         *reinterpret_cast<u32x4*>(o + e * p.os1) = lo[e];  // cached: attention reads the rotated rows next
         *reinterpret_cast<u32x4*>(o + e * p.os1 + HALF) = hi[e];

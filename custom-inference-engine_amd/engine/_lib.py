@@ -16,7 +16,7 @@ import torch
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("CIE_ATTN_LIB", os.path.join(PKG_ROOT, "libcie_attn.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CIE_OK = 0
 CIE_EINVAL = -1
@@ -26,6 +26,7 @@ CIE_EWORKSPACE = -4
 CIE_ELAUNCH = -5
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+TABLE_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 EXPORTED_SYMBOLS = (
     "cie_abi_version",
@@ -75,26 +76,26 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cie_kv_append.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]
     lib.cie_kv_append.restype = _i
-    lib.cie_rope_apply.argtypes = [_vp, _vp, _i64p, _i64p, _vp, ctypes.c_int64, _vp, _vp, _i, _vp,
+    lib.cie_rope_apply.argtypes = [_vp, _vp, _i64p, _i64p, _vp, ctypes.c_int64, _vp, _vp, _i, _i, _vp,
                                    _i, _i, _i, _i, _i, _vp]
     lib.cie_rope_apply.restype = _i
     lib.cie_flash_fwd_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
-                                       _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp, _vp, _i, _vp, _vp]
+                                       _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp, _vp, _i, _i, _vp, _vp]
     lib.cie_flash_fwd_rope.restype = _i
     lib.cie_paged_fwd_rope.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
                                        _i64p, _i64p, _i64p, _i64p,
                                        _i, _i, _i, _i, _i, _i, _i, _i, _i,
-                                       ctypes.c_float, _i, _i, _vp, _vp, _i, _vp]
+                                       ctypes.c_float, _i, _i, _vp, _vp, _i, _i, _vp]
     lib.cie_paged_fwd_rope.restype = _i
     lib.cie_paged_fwd_append.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
                                          _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
                                          _i, _i, _i, _i, _i, _i, _i, _i, _i,
                                          ctypes.c_float, _i, _i, _vp]
     lib.cie_paged_fwd_append.restype = _i
-    lib.cie_paged_fwd_append_rope.argtypes = lib.cie_paged_fwd_append.argtypes[:-1] + [_vp, _vp, _i, _vp]
+    lib.cie_paged_fwd_append_rope.argtypes = lib.cie_paged_fwd_append.argtypes[:-1] + [_vp, _vp, _i, _i, _vp]
     lib.cie_paged_fwd_append_rope.restype = _i
     lib.cie_kv_append_rope.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
-                                       _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i64p, _vp]
+                                       _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i64p, _vp]
     lib.cie_kv_append_rope.restype = _i
     lib.cie_int8_matmul_workspace_bytes.argtypes = [_i, _i, _i]
     lib.cie_int8_matmul_workspace_bytes.restype = ctypes.c_size_t

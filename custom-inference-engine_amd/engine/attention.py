@@ -58,20 +58,25 @@ def _output(out: torch.Tensor | None, shape: tuple[int, ...], q: torch.Tensor) -
     return out
 
 
-def rope_args(rope: tuple[torch.Tensor, torch.Tensor], D: int, device: torch.device) -> tuple[int, int, int]:
-    """Validate RoPE tables (cos, sin: fp32 (rows, D/2), contiguous, on
-    ``device``, as ``RotaryEmbedding`` holds them) and return their
-    pointers and row count for the library."""
+def rope_args(rope: tuple[torch.Tensor, torch.Tensor], D: int, device: torch.device) -> tuple[int, int, int, int]:
+    """Validate RoPE tables (cos, sin: (rows, D/2), contiguous, on ``device``,
+    fp32 as ``RotaryEmbedding`` builds them or fp16 / bf16 as the reference
+    engine's ``cast_non_quantized_params`` leaves them) and return their
+    pointers, row count and table dtype code for the library."""
     cos, sin = rope
     for name, t in (("cos", cos), ("sin", sin)):
         if not t.is_cuda or t.device != device:
             raise RuntimeError(f"rope {name} table must be on {device}")
-        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != D // 2 or not t.is_contiguous():
-            raise ValueError(f"rope {name} table must be contiguous fp32 (rows, {D // 2}), got "
+        if t.dtype not in _lib.TABLE_DTYPE_CODES or t.dim() != 2 or t.shape[1] != D // 2 or not t.is_contiguous():
+            raise ValueError(f"rope {name} table must be contiguous fp32, fp16 or bf16 (rows, {D // 2}), got "
                              f"{t.dtype} {tuple(t.shape)}")
-    if cos.shape != sin.shape or cos.shape[0] < 1:
-        raise ValueError(f"rope tables differ or are empty: {tuple(cos.shape)}, {tuple(sin.shape)}")
-    return cos.data_ptr(), sin.data_ptr(), int(cos.shape[0])
+    if cos.shape != sin.shape or cos.shape[0] < 1 or cos.dtype != sin.dtype:
+        raise ValueError(f"rope tables differ or are empty: {tuple(cos.shape)} {cos.dtype}, "
+                         f"{tuple(sin.shape)} {sin.dtype}")
+    for t in (cos, sin):
+        if t.data_ptr() % 16:
+            raise ValueError("rope tables must start 16-byte aligned")
+    return cos.data_ptr(), sin.data_ptr(), int(cos.shape[0]), _lib.TABLE_DTYPE_CODES[cos.dtype]
 
 
 def flash_attention(
@@ -131,7 +136,7 @@ def flash_attention(
                 B, H, Hk, M, N, D, float(scale), 1 if causal else 0,
                 _lib.DTYPE_CODES[q.dtype], _lib.stream_handle(q.device))
         else:
-            cos_p, sin_p, rows = rope_args(rope, D, q.device)
+            cos_p, sin_p, rows, tdt = rope_args(rope, D, q.device)
             pos_p = None
             if q_pos0 is not None:
                 if not q_pos0.is_cuda or q_pos0.device != q.device or q_pos0.dtype != torch.int32 \
@@ -142,7 +147,7 @@ def flash_attention(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                 _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
                 B, H, Hk, M, N, D, float(scale), 1 if causal else 0,
-                _lib.DTYPE_CODES[q.dtype], cos_p, sin_p, rows, pos_p, _lib.stream_handle(q.device))
+                _lib.DTYPE_CODES[q.dtype], cos_p, sin_p, rows, tdt, pos_p, _lib.stream_handle(q.device))
     _lib.check(rc)
     return out
 
@@ -157,14 +162,20 @@ def paged_workspace_bytes(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size:
 
 
 # Workspaces, one per (device, stream): calls on one stream run in order, so
-# they can share it.
+# they can share it. A workspace outgrown by a larger call is retired, never
+# freed: a HIP graph captured earlier may still hold its address, and its
+# replays must not write into memory the caching allocator has handed to
+# another tensor.
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_RETIRED_WORKSPACES: list[torch.Tensor] = []
 
 
 def _cached_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
@@ -253,6 +264,10 @@ def paged_attention(
     lens = context_lens.to(torch.int32).contiguous()
     max_blocks = bt.shape[1]
     q = _kernel_layout(q)
+    if new_kv is not None and (_kernel_layout(k_cache) is not k_cache or _kernel_layout(v_cache) is not v_cache):
+        # the fused append writes the pools in place: a copy would drop the new tokens
+        raise ValueError("paged_attention(new_kv=...) needs pools with a unit last stride, 16-byte aligned rows "
+                         "and outer strides in multiples of 8 elements")
     k_cache, v_cache = _kernel_layout(k_cache), _kernel_layout(v_cache)
     mc = int(max_context or 0)
     ws_bytes = int(lib.cie_paged_workspace_bytes(B, Hq, Hk, Lq, D, mc, block_size, max_blocks))

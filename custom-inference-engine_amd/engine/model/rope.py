@@ -51,7 +51,7 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions:
     B, H, L, D = x.shape
     _check_head_dim(D)
     _check_dtype(x)
-    cos_p, sin_p, rows = rope_args((cos, sin), D, x.device)
+    cos_p, sin_p, rows, tdt = rope_args((cos, sin), D, x.device)
     pos_p, pos_bs = None, 0
     if positions is not None:
         if positions.dim() == 1 and positions.shape[0] == L:
@@ -71,7 +71,7 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions:
     lib = _lib.load()
     with torch.cuda.device(x.device):
         rc = lib.cie_rope_apply(src.data_ptr(), dst.data_ptr(), _lib.strides(src), _lib.strides(dst), pos_p, pos_bs,
-                                cos_p, sin_p, rows, status.data_ptr() if status is not None else None,
+                                cos_p, sin_p, rows, tdt, status.data_ptr() if status is not None else None,
                                 B, H, L, D, _lib.DTYPE_CODES[x.dtype], _lib.stream_handle(x.device))
     _lib.check(rc)
     if dst is not out:

@@ -14,7 +14,10 @@ import torch
 from engine import _lib
 
 _SCALE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+# One split-K workspace per (device, stream); an outgrown one is retired, not
+# freed, since a HIP graph captured earlier may still write to it.
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_RETIRED_WORKSPACES: list[torch.Tensor] = []
 
 
 def int8_matmul_workspace_bytes(M: int, N: int, K: int) -> int:
@@ -23,12 +26,26 @@ def int8_matmul_workspace_bytes(M: int, N: int, K: int) -> int:
     return int(_lib.load().cie_int8_matmul_workspace_bytes(M, N, K))
 
 
+def _aligned_rows(t: torch.Tensor, elems: int) -> torch.Tensor:
+    """``t`` (rows, K) with 16-byte aligned rows (row stride a multiple of
+    ``elems`` elements, unit column stride): ``t`` itself when it already is,
+    else a copy into a buffer whose rows are padded to that multiple."""
+    if t.stride(1) == 1 and t.stride(0) % elems == 0 and t.data_ptr() % 16 == 0 and t.stride(0) >= t.shape[1]:
+        return t
+    rows, K = t.shape
+    buf = torch.empty((rows, -(-K // elems) * elems), dtype=t.dtype, device=t.device)
+    buf[:, :K] = t
+    return buf[:, :K]
+
+
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
     if nbytes == 0:
         return None
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
@@ -53,13 +70,14 @@ def int8_matmul(x: torch.Tensor, w_int8: torch.Tensor, scales: torch.Tensor,
         raise ValueError(f"in_features mismatch: x has {x.shape[-1]}, w_int8 has {K}")
     if scales.shape[0] != N:
         raise ValueError(f"scales must have shape ({N},), got {tuple(scales.shape)}")
-    if K % 64:
-        raise ValueError(f"in_features must be a multiple of 64, got {K}")
-    x2 = x.reshape(-1, K)
-    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-        x2 = x2.contiguous()
-    w = w_int8 if (w_int8.stride(1) == 1 and w_int8.stride(0) % 16 == 0 and w_int8.data_ptr() % 16 == 0) \
-        else w_int8.contiguous()
+    if K < 1:
+        raise ValueError(f"in_features must be positive, got {K}")
+    # the kernels read rows in 16-byte pieces: rows that do not start 16-byte
+    # aligned (e.g. K = 100 int8 weights) are copied into padded rows first;
+    # any K is accepted, its tail past the kernels' step is masked as the
+    # reference masks it (kernels/int8_matmul.py:43-50)
+    x2 = _aligned_rows(x.reshape(-1, K), 8)
+    w = _aligned_rows(w_int8, 16)
     s = scales if scales.dtype in _SCALE_CODES else scales.float()
     s = s.contiguous()
     b = None

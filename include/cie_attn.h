@@ -45,9 +45,12 @@
 extern "C" {
 #endif
 
-#define CIE_ABI_VERSION 1
+#define CIE_ABI_VERSION 2
 
 enum cie_dtype { CIE_DTYPE_F16 = 0, CIE_DTYPE_BF16 = 1 };
+
+/* Element type of the rotary cos / sin tables. */
+enum cie_table_dtype { CIE_TABLE_F16 = 0, CIE_TABLE_BF16 = 1, CIE_TABLE_F32 = 2 };
 
 enum cie_status {
   CIE_OK = 0,
@@ -149,14 +152,19 @@ int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
 /*
  * Rotary position embedding (RoPE).
  *
- * rope_cos, rope_sin: fp32 device tables of shape (rope_rows, D/2), row-major
- * and 16-byte aligned: RotaryEmbedding's cos / sin buffers
- * (engine/model/rope.py:12-16, built by kernels/ref/rope_apply_ref.py:6-19).
+ * rope_cos, rope_sin: device tables of shape (rope_rows, D/2), row-major and
+ * 16-byte aligned, of element type rope_dtype (CIE_TABLE_*):
+ * RotaryEmbedding's cos / sin buffers (engine/model/rope.py:12-16, built in
+ * fp32 by kernels/ref/rope_apply_ref.py:6-19; the reference engine casts
+ * them to the activation dtype, engine/runtime.py:22-37).
  * Every entry point below rotates exactly as apply_rotary_ref
  * (kernels/ref/rope_apply_ref.py:46-53): x1 = x[:D/2], x2 = x[D/2:],
- * rot1 = x1*c - x2*s, rot2 = x1*s + x2*c with each product, difference and
- * sum rounded to fp32 (no fused multiply-add) and the result rounded to the
- * element type, so its output is bit-identical to the reference's.
+ * rot1 = x1*c - x2*s, rot2 = x1*s + x2*c, with torch's arithmetic for the
+ * two operand types: tables of the element type -> each product, difference
+ * and sum rounded to the element type; fp32 tables (or 16-bit tables of the
+ * other 16-bit type) -> each rounded to fp32 and the result rounded to the
+ * element type. No fused multiply-add, so the output is bit-identical to the
+ * reference's.
  */
 
 /*
@@ -172,7 +180,7 @@ int cie_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
  */
 int cie_rope_apply(const void* x, void* out, const int64_t* x_stride, const int64_t* out_stride,
                    const int32_t* positions, int64_t pos_batch_stride,
-                   const float* rope_cos, const float* rope_sin, int rope_rows,
+                   const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                    uint32_t* status, int B, int H, int L, int D, int dtype, void* stream);
 
 /*
@@ -191,7 +199,7 @@ int cie_flash_fwd_rope(const void* q, const void* k, const void* v, void* o,
                        const int64_t* v_stride, const int64_t* o_stride,
                        int B, int Hq, int Hk, int Lq, int Lk, int D,
                        float scale, int causal, int dtype,
-                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                        const int32_t* q_pos0, void* stream);
 
 /*
@@ -212,7 +220,7 @@ int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
                        int B, int Hq, int Hk, int Lq, int D,
                        int num_blocks, int block_size, int max_blocks_per_seq,
                        int max_context, float scale, int causal, int dtype,
-                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                        void* stream);
 
 /*
@@ -233,7 +241,7 @@ int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
  * Reference: engine/model/block.py:57-71 (append, then gather + attend).
  */
 int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
-                         const void* k_cache, const void* v_cache,
+                         void* k_cache, void* v_cache,
                          const int32_t* block_tables, const int32_t* context_lens,
                          void* o, void* workspace, size_t workspace_bytes,
                          const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
@@ -249,11 +257,12 @@ int cie_paged_fwd_append(const void* q, const void* k_new, const void* v_new,
  * used and as it is written into the pool, q as it is loaded. Pool and
  * output are bit-identical to cie_kv_append_rope (start = context_lens[b] -
  * Lq) followed by cie_paged_fwd_rope. A position outside [0, rope_rows)
- * gives NaN rows.
+ * gives NaN output rows, and neither K nor V of that token is written (as
+ * cie_kv_append_rope leaves the pool; there is no status word here).
  * Reference: engine/model/block.py:53-54 (RoPE) and :57-71.
  */
 int cie_paged_fwd_append_rope(const void* q, const void* k_new, const void* v_new,
-                              const void* k_cache, const void* v_cache,
+                              void* k_cache, void* v_cache,
                               const int32_t* block_tables, const int32_t* context_lens,
                               void* o, void* workspace, size_t workspace_bytes,
                               const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
@@ -261,7 +270,7 @@ int cie_paged_fwd_append_rope(const void* q, const void* k_new, const void* v_ne
                               int B, int Hq, int Hk, int Lq, int D,
                               int num_blocks, int block_size, int max_blocks_per_seq,
                               int max_context, float scale, int causal, int dtype,
-                              const float* rope_cos, const float* rope_sin, int rope_rows,
+                              const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                               void* stream);
 
 /*
@@ -282,17 +291,22 @@ int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void
                        const int32_t* block_tables, const int32_t* cu_new, const int32_t* start,
                        uint32_t* status, int B, int T, int max_new, int Hk, int D,
                        int num_blocks, int block_size, int max_blocks_per_seq, int dtype,
-                       const float* rope_cos, const float* rope_sin, int rope_rows,
+                       const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
                        void* k_out, const int64_t* k_out_stride, void* stream);
 
 /*
  * INT8-weight linear layer: y = (x . w_int8^T) * scales[n] (+ bias[n]).
  *   x: (M, K) fp16 / bf16 (dtype), row stride x_row_stride elements
+ *        (a multiple of 8: rows start 16-byte aligned)
  *   w_int8: (N, K) int8, row stride w_row_stride bytes (multiple of 16)
  *   scales: (N,) per output channel, fp16 / bf16 / fp32 (scale_dtype 0 / 1 / 2)
  *   bias: (N,) in x's dtype, or NULL
  *   y: (M, N) in x's dtype, row stride y_row_stride elements (8-byte aligned)
- * K must be a multiple of 64. The products x * w are exact and summed in
+ * Any K >= 1: each kernel's vector loop covers the largest prefix of K its
+ * step divides and the remaining k (fewer than 64) of every output are added
+ * in the epilogue, as the reference masks the K tail of its last tile
+ * (kernels/int8_matmul.py:43-50); nothing past column K of a row is read.
+ * The products x * w are exact and summed in
  * fp32; the sum is multiplied by the scale once and rounded to x's dtype,
  * then the bias is added in x's dtype (rounded again), as the reference does.
  * workspace: cie_int8_matmul_workspace_bytes(M, N, K) bytes, 16-byte

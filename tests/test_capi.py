@@ -127,7 +127,7 @@ def _paged_append(rope=False, **over):
             a["nb"], a["bs"], a["mb"], a["mc"], a["scale"], a["causal"], a["dtype"])
     lib = _lib.load()
     if rope:
-        return lib.cie_paged_fwd_append_rope(*head, FAKE, FAKE, 4096, None)
+        return lib.cie_paged_fwd_append_rope(*head, FAKE, FAKE, 4096, 2, None)
     return lib.cie_paged_fwd_append(*head, None)
 
 

@@ -55,7 +55,14 @@ def _exact_case(M, N, K, dtype, seed, bias):
                                    # the dot-product kernel (M <= 4): ragged N, K tails within a 1 KiB chunk
                                    (2, 300, 640), (3, 1001, 2112), (4, 130, 1088), (1, 7, 64), (1, 11008, 4096),
                                    # the streaming kernel at 8 / 16 / 32 / 64 staged rows, K tails within a pass
-                                   (8, 4096, 4096), (12, 520, 1216), (40, 333, 1088), (64, 1000, 4160), (65, 512, 1024)])
+                                   (8, 4096, 4096), (12, 520, 1216), (40, 333, 1088), (64, 1000, 4160), (65, 512, 1024),
+                                   # any K (the reference masks the K tail, kernels/int8_matmul.py:43-50):
+                                   # K below one step of each kernel, K tails of 4 / 32 / 36 past a step,
+                                   # rows not 16-byte aligned (K = 100, 4100, 17: padded copies)
+                                   (1, 32, 32), (1, 17, 8), (1, 4096, 100), (1, 300, 4100), (2, 64, 32),
+                                   (3, 300, 96), (12, 520, 100), (40, 333, 4100), (64, 128, 32), (64, 96, 17),
+                                   (65, 512, 4100), (512, 1024, 4100), (100, 127, 96), (300, 96, 32), (2048, 256, 100),
+                                   (130, 4096, 4132)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
     for bias in (False, True):
@@ -66,7 +73,8 @@ def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,N,K", [(1, 512, 4096), (3, 256, 1600), (7, 256, 512), (64, 1024, 2048), (300, 384, 4096)])
+@pytest.mark.parametrize("M,N,K", [(1, 512, 4096), (3, 256, 1600), (7, 256, 512), (64, 1024, 2048), (300, 384, 4096),
+                                   (1, 512, 100), (33, 256, 4100), (300, 384, 96), (5, 64, 32)])
 def test_random_activations_within_rounding(M, N, K, dtype):
     g = torch.Generator().manual_seed(M * 7 + K)
     x = torch.randn(M, K, generator=g).to(dtype)
@@ -117,6 +125,24 @@ def test_int8_linear_close_to_float_layer():
     ref = int8_matmul_kernel_order_ref(x.cpu(), qlin.weight_int8.cpu(), qlin.scales.cpu(), qlin.bias.detach().cpu())
     atol, rtol = TOL[torch.float16]
     assert ((y_q.cpu().float() - ref.float()).abs() <= atol + rtol * ref.float().abs()).all()
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_reference_tiny_model_layers(M):
+    """Every Int8Linear of the reference's tiny test model
+    (tests/conftest.py:30-43: hidden 32, 2 heads of 16, intermediate 64,
+    vocab 32): q/k/v/o 32 -> 32, gate/up 32 -> 64, down 64 -> 32, lm head
+    32 -> 32; a decode token (M = 1) and an 8-token prefill, against the
+    oracle at the reference's tolerance."""
+    torch.manual_seed(M)
+    for fin, fout in ((32, 32), (32, 64), (64, 32)):
+        lin = torch.nn.Linear(fin, fout, bias=False).to(device=DEV, dtype=torch.float16)
+        qlin = quantize_linear(lin).to(DEV)
+        x = torch.randn(1, M, fin, device=DEV, dtype=torch.float16)
+        y = qlin(x)
+        assert y.shape == (1, M, fout)
+        ref = int8_matmul_ref(x.cpu().reshape(M, fin), qlin.weight_int8.cpu(), qlin.scales.cpu())
+        assert (y.cpu().reshape(M, fout).float() - ref.float()).abs().max().item() < 1e-3
 
 
 def test_repeated_calls_are_deterministic():

@@ -178,7 +178,7 @@ def _call(**over):
 
 
 @pytest.mark.parametrize("over,code", [
-    (dict(dtype=2), -3), (dict(sdt=3), -3), (dict(K=100, xs=112, wsr=112), -1), (dict(M=-1), -1),
+    (dict(dtype=2), -3), (dict(sdt=3), -3), (dict(K=0), -1), (dict(M=-1), -1), (dict(K=100, xs=100), -1),
     (dict(x=0), -1), (dict(w=FAKE + 4), -1), (dict(s=0), -1), (dict(s=FAKE + 1), -1), (dict(b=FAKE + 1), -1),
     (dict(xs=4100), -1), (dict(wsr=4104), -1), (dict(ys=100), -1), (dict(y=FAKE + 4), -1), (dict(ws=0), -4), (dict(wsb=16), -4),
 ])
@@ -197,4 +197,5 @@ def test_int8_matmul_empty_and_workspace_query():
     assert lib.cie_int8_matmul_workspace_bytes(64, 4096, 4096) == 0       # decode shapes stream the weights
     assert lib.cie_int8_matmul_workspace_bytes(128, 4096, 4096) > 0       # few tiles: split K
     assert lib.cie_int8_matmul_workspace_bytes(4096, 4096, 4096) == 0     # enough tiles: no split
-    assert lib.cie_int8_matmul_workspace_bytes(64, 4096, 100) == 0        # unsupported K
+    assert lib.cie_int8_matmul_workspace_bytes(64, 4096, 100) == 0        # any K; streaming needs none
+    assert lib.cie_int8_matmul_workspace_bytes(128, 4096, 4100) > 0       # any K; split like K = 4096

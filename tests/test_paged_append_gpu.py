@@ -101,16 +101,24 @@ def test_fused_append_invalid_context_and_block_id():
         assert torch.equal(k1[blk], kp[blk]) and torch.equal(v1[blk], vp[blk]), blk
 
 
+@pytest.mark.parametrize("tables", ["fp32", "cast"])
 @pytest.mark.parametrize("Lq", [1, 5])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_fused_append_with_rope_equals_rotating_append_then_attend(Lq, D, dtype):
+def test_fused_append_with_rope_equals_rotating_append_then_attend(Lq, D, dtype, tables):
     """q and k_new un-rotated: the fused pair rotates the new K rows in LDS
     and on their way into the pool, bit-identical to kv_append(rope=) then
-    paged_attention(rope=)."""
+    paged_attention(rope=); with fp32 tables and with tables cast to the
+    activation dtype as the reference engine casts them
+    (engine/runtime.py:35-37). Every head_dim covers one swizzle family of
+    the in-LDS rotation."""
     from engine.model.rope import RotaryEmbedding
 
-    emb = RotaryEmbedding(D, 8192).to(DEV)
+    emb = RotaryEmbedding(D, 8192)
+    if tables == "cast":
+        for name, b in list(emb.named_buffers(recurse=False)):
+            setattr(emb, name, b.to(dtype))
+    emb = emb.to(DEV)
     lens = [Lq, 40 + Lq, 700, 2049, 4096, 33]
     q, kp, vp, bt, lt = make_paged(lens, Lq, D, dtype, 16, Hq=8, Hk=2, seed=D + Lq, vscale=0.5)
     k_new, v_new = _new_rows(len(lens), Lq, 2, D, dtype, seed=21 + Lq)
@@ -122,6 +130,50 @@ def test_fused_append_with_rope_equals_rotating_append_then_attend(Lq, D, dtype)
     o1, k1, v1 = _fused(q, kp, vp, bt, lt, k_new, v_new, rope=emb.tables)
     assert torch.equal(k1, kd.cpu()) and torch.equal(v1, vd.cpu()), "pool after the rotating fused append differs"
     assert torch.equal(o1, o2), (o1.float() - o2.float()).abs().max().item()
+
+
+def test_fused_append_with_rope_position_outside_table_writes_nothing():
+    """New tokens whose positions lie outside the rotary tables: their query
+    rows are NaN and neither their K nor their V reaches the pool, as the
+    rotating append leaves the pool (kv_append(rope=) writes neither). Rows
+    of the same sequence whose positions are inside see only keys inside."""
+    from engine.model.rope import build_rope_cache
+
+    Lq, D, dtype = 5, 64, torch.float16
+    lens = [40, 300]  # sequence 1's new tokens sit at positions 295..299; the tables hold 0..296
+    q, kp, vp, bt, lt = make_paged(lens, Lq, D, dtype, 16, seed=31)
+    k_new, v_new = _new_rows(len(lens), Lq, 2, D, dtype, seed=32)
+    cos, sin = build_rope_cache(297, D)
+    o1, k1, v1 = _fused(q, kp, vp, bt, lt, k_new, v_new, rope=(cos.to(DEV), sin.to(DEV)))
+    assert not torch.isnan(o1[0]).any()
+    assert not torch.isnan(o1[1, :, :2]).any() and torch.isnan(o1[1, :, 2:]).all()
+    for pos in range(295, 300):
+        blk, off = int(bt[1, pos // 16]), pos % 16
+        if pos < 297:  # inside the tables: written
+            assert torch.equal(v1[blk, off], v_new[Lq + pos - 295])
+        else:  # outside: the pool keeps its old rows
+            assert torch.equal(k1[blk, off], kp[blk, off]) and torch.equal(v1[blk, off], vp[blk, off]), pos
+
+
+def test_fused_append_rejects_pools_it_cannot_write_in_place():
+    """The fused append writes the pools in place: a pool view the kernels
+    cannot address directly (here 8-byte aligned) is rejected rather than
+    copied, which would drop the appended tokens."""
+    q, kp, vp, bt, lt = make_paged([40], 1, 64, torch.float16, 16)
+    k_new, v_new = _new_rows(1, 1, 2, 64, torch.float16, seed=1)
+    nb = kp.shape[0]
+    flat_k = torch.zeros(kp.numel() + 4, dtype=torch.float16, device=DEV)
+    flat_v = torch.zeros_like(flat_k)
+    kd = flat_k[4:].view(nb, 16, 2, 64)  # 8 bytes past a 16-byte boundary
+    vd = flat_v[4:].view(nb, 16, 2, 64)
+    kd.copy_(kp.to(DEV))
+    vd.copy_(vp.to(DEV))
+    with pytest.raises(ValueError):
+        paged_attention(q.to(DEV), kd, vd, bt.to(DEV), lt.to(DEV), new_kv=(k_new.to(DEV), v_new.to(DEV)))
+    # without the append the same views are read through a copy, correctly
+    out = paged_attention(q.to(DEV), kd, vd, bt.to(DEV), lt.to(DEV))
+    ref = paged_attention_ref(q.float(), kp.float(), vp.float(), bt, lt, causal=True)
+    assert_close(out.cpu(), ref, TOL[torch.float16], "misaligned pool read through a copy")
 
 
 def test_fused_append_rejects_bad_shapes():

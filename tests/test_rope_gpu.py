@@ -28,16 +28,27 @@ DEV = "cuda"
 TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
 
 
-def _tables(n, D, theta=10000.0):
+def _tables(n, D, theta=10000.0, tdt=torch.float32):
+    """cos, sin on the host and on the GPU, in table dtype tdt: fp32 as
+    built, or cast as the reference engine casts RotaryEmbedding's buffers
+    (engine/runtime.py:35-37)."""
     c, s = build_rope_cache(n, D, theta)
+    c, s = c.to(tdt), s.to(tdt)
     return c, s, c.to(DEV), s.to(DEV)
 
 
+def _tdt(kind, dtype):
+    """Table dtype for x of `dtype`: fp32, the same 16-bit type, or the other one."""
+    return {"fp32": torch.float32, "same": dtype,
+            "other": torch.bfloat16 if dtype == torch.float16 else torch.float16}[kind]
+
+
+@pytest.mark.parametrize("tables", ["fp32", "same", "other"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
-def test_rope_apply_bit_exact(D, dtype):
+def test_rope_apply_bit_exact(D, dtype, tables):
     B, H, L = 2, 3, 37
-    c, s, cd, sd = _tables(4096, D)
+    c, s, cd, sd = _tables(4096, D, tdt=_tdt(tables, dtype))
     g = torch.Generator().manual_seed(D)
     x = (torch.randn(B, H, L, D, generator=g) * 3).to(dtype)
     pos1 = torch.randint(0, 4096, (L,), generator=g)
@@ -62,6 +73,30 @@ def test_rope_apply_strided_in_place_and_module():
     x = torch.randn(1, 4, 5, D, generator=g).bfloat16()
     assert torch.equal(emb.apply(x.to(DEV), torch.tensor([0, 1, 2, 3, 4], device=DEV)).cpu(),
                        rope_ref(x, c, s, torch.arange(5)))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_module_after_reference_engine_cast(dtype):
+    """RotaryEmbedding whose buffers went through the reference engine's cast
+    (cast_non_quantized_params: every floating buffer to the activation
+    dtype) rotates bit-identically to apply_rotary_ref with those tables."""
+    D = 64
+    emb = RotaryEmbedding(D, 1024)
+    for name, b in list(emb.named_buffers(recurse=False)):
+        if b.is_floating_point():
+            setattr(emb, name, b.to(dtype))
+    c, s = emb.cos.clone(), emb.sin.clone()
+    emb = emb.to(DEV)
+    assert emb.cos.dtype == dtype
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(2, 4, 33, D, generator=g) * 2).to(dtype)
+    pos = torch.randint(0, 1024, (2, 33), generator=g)
+    got = emb.apply(x.to(DEV), pos.to(DEV)).cpu()
+    assert torch.equal(got, rope_ref(x, c, s, pos))
+    # the reference's expression, evaluated by torch on these 16-bit tensors
+    cc, ss = c[pos].reshape(2, 1, 33, D // 2), s[pos].reshape(2, 1, 33, D // 2)
+    x1, x2 = x[..., :D // 2], x[..., D // 2:]
+    assert torch.equal(got, torch.cat([x1 * cc - x2 * ss, x1 * ss + x2 * cc], -1))
 
 
 def test_rope_apply_out_of_range_positions():
@@ -89,12 +124,13 @@ def _batch_tables(lens, starts, bs, seed, extra=4):
     return nb, tables, bt
 
 
+@pytest.mark.parametrize("tables", ["fp32", "same"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("Hk,D", [(8, 64), (2, 16), (4, 128), (1, 256)])
-def test_rotary_append_bit_exact(Hk, D, dtype):
+def test_rotary_append_bit_exact(Hk, D, dtype, tables):
     bs = 16
     lens, starts = [1, 37, 0, 64, 5], [0, 3, 9, 100, 15]
-    c, s, cd, sd = _tables(1024, D)
+    c, s, cd, sd = _tables(1024, D, tdt=_tdt(tables, dtype))
     nb, tables, bt = _batch_tables(lens, starts, bs, seed=D)
     g = torch.Generator().manual_seed(Hk)
     kp = torch.randn(nb, bs, Hk, D, generator=g).to(dtype)
@@ -138,11 +174,12 @@ def test_rotary_append_position_outside_table_writes_nothing():
     assert (vd[blk, :2] == 1).all() and (vd[blk, 2:] == 0).all() and (kd[blk, 2:] == 0).all()
 
 
+@pytest.mark.parametrize("tables", ["fp32", "same"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("D", [16, 64, 128])
-def test_flash_with_fused_q_rope(D, dtype):
+def test_flash_with_fused_q_rope(D, dtype, tables):
     B, Hq, Hk, L = 2, 8, 2, 200
-    c, s, cd, sd = _tables(2048, D)
+    c, s, cd, sd = _tables(2048, D, tdt=_tdt(tables, dtype))
     g = torch.Generator().manual_seed(11 + D)
     q = torch.randn(B, Hq, L, D, generator=g).to(dtype)
     k = torch.randn(B, Hk, L, D, generator=g).to(dtype)
@@ -166,13 +203,14 @@ def test_flash_with_fused_q_rope(D, dtype):
     assert torch.equal(f0[0], fused[0])
 
 
+@pytest.mark.parametrize("tables", ["fp32", "same"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("Lq,D", [(1, 64), (5, 128), (1, 16), (3, 256)])
-def test_paged_with_fused_q_rope(Lq, D, dtype):
+def test_paged_with_fused_q_rope(Lq, D, dtype, tables):
     Hq, Hk, bs = 8, 2, 16
     ctx = [40, 1000, 5, 333, 17 + Lq]
     B = len(ctx)
-    c, s, cd, sd = _tables(2048, D)
+    c, s, cd, sd = _tables(2048, D, tdt=_tdt(tables, dtype))
     nb, tables, bt = _batch_tables(ctx, [0] * B, bs, seed=Lq + D)
     g = torch.Generator().manual_seed(D)
     kp = torch.randn(nb, bs, Hk, D, generator=g).to(dtype)
@@ -192,8 +230,9 @@ def test_paged_with_fused_q_rope(Lq, D, dtype):
         assert (fused[b:b + 1].float().cpu() - ref).abs().max().item() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("cast", [False, True])
 @pytest.mark.parametrize("L,dtype", [(1, torch.float16), (4, torch.bfloat16), (96, torch.float16)])
-def test_attention_section_with_rope_matches_reference_order(L, dtype):
+def test_attention_section_with_rope_matches_reference_order(L, dtype, cast):
     """Prefill (fresh sequences, L=96), decode (L=1) and verify (L=4) through
     attention_section with un-rotated q, k and the model's tables, against
     the reference's per-sequence order on the oracle: rotate q and k at
@@ -203,6 +242,9 @@ def test_attention_section_with_rope_matches_reference_order(L, dtype):
 
     B, Hq, Hk, D, bs = 3, 8, 2, 64, 16
     emb = RotaryEmbedding(D, 4096)
+    if cast:  # the reference engine's cast of every floating buffer (engine/runtime.py:35-37)
+        for name, b in list(emb.named_buffers(recurse=False)):
+            setattr(emb, name, b.to(dtype))
     c, s = emb.cos, emb.sin
     emb = emb.to(DEV)
     cache = PagedKVCache(KVCacheConfig(num_layers=1, num_kv_heads=Hk, head_dim=D, num_blocks=120, block_size=bs,
