@@ -328,6 +328,33 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
                     max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0});
 }
 
+int cie_paged_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* context_lens, void* o,
+                          const int64_t* q_stride, const int64_t* kc_stride,
+                          const int64_t* vc_stride, const int64_t* o_stride,
+                          int B, int Hq, int Hk, int Lq, int D,
+                          int num_blocks, int block_size, int max_blocks_per_seq,
+                          int max_context, float scale, int causal, int dtype,
+                          void* stream) {
+  // the workspace this shape needs must fit the static array; checked
+  // before any HIP call
+  const size_t need = cie_paged_workspace_bytes(B, Hq, Hk, Lq, D, max_context, block_size, max_blocks_per_seq);
+  if (need > cie::kPagedScratchBytes)
+    return fail(CIE_EWORKSPACE, "this shape needs %zu bytes of workspace, more than the %zu-byte static workspace "
+                "of cie_paged_fwd_noalloc; use cie_paged_fwd with a caller workspace", need,
+                cie::kPagedScratchBytes);
+  if ((int64_t)B * Hq * Lq <= 0 || need == 0)  // empty, or a shape cie_paged_fwd rejects: same result, no lookup
+    return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, nullptr, 0, q_stride, kc_stride,
+                      vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
+                      max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0});
+  void* ws = nullptr;
+  const hipError_t e = cie::paged_scratch_ptr(&ws);
+  if (e != hipSuccess) return fail(CIE_ELAUNCH, "static workspace lookup failed: %s", hipGetErrorString(e));
+  return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, ws, cie::kPagedScratchBytes, q_stride,
+                    kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
+                    max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0});
+}
+
 int cie_paged_fwd_rope(const void* q, const void* k_cache, const void* v_cache,
                        const int32_t* block_tables, const int32_t* context_lens,
                        void* o, void* workspace, size_t workspace_bytes,

@@ -187,4 +187,10 @@ hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, int dtype
 hipError_t launch_rope(const RopeParams& p, int dtype, int D, hipStream_t stream);
 hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, hipStream_t stream);
 
+// Bytes of the static device workspace behind cie_paged_fwd_noalloc.
+constexpr size_t kPagedScratchBytes = (size_t)16 << 20;
+// Device address of that workspace on the current device, looked up once
+// per device (the host-side symbol is not a device address). Thread-safe.
+hipError_t paged_scratch_ptr(void** ptr);
+
 }  // namespace cie

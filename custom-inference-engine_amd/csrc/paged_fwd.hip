@@ -41,6 +41,8 @@
 // [0, ctx_limit] or a block id outside [0, num_blocks) makes that sequence's
 // output NaN.
 #include <climits>
+#include <map>
+#include <mutex>
 
 #include "kernels.hpp"
 #include "rope.hpp"
@@ -833,6 +835,32 @@ static hipError_t launch_paged_d(const PagedParams& p, int D, size_t lds, hipStr
 
 hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds, hipStream_t stream) {
   return dtype == 0 ? launch_paged_d<0>(p, D, lds, stream) : launch_paged_d<1>(p, D, lds, stream);
+}
+
+// Static workspace of the allocation-free paged entry: one copy per GPU,
+// loaded with the code object and held until the process ends. Every call
+// on a device shares it, so calls that overlap on one device race; nothing
+// in it needs to start at zero (the main pass writes every piece descriptor
+// the merge pass reads, and every partial state before its descriptor).
+static __device__ __align__(256) unsigned char paged_scratch[kPagedScratchBytes];
+
+hipError_t paged_scratch_ptr(void** ptr) {
+  static std::mutex mu;
+  static std::map<int, void*> per_device;  // the array's address on each device
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = per_device.find(dev);
+  if (it == per_device.end()) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(paged_scratch));  // with `dev` current
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    it = per_device.emplace(dev, p).first;
+  }
+  *ptr = it->second;
+  return hipSuccess;
 }
 
 }  // namespace cie

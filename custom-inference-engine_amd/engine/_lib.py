@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "cie_flash_fwd",
     "cie_paged_workspace_bytes",
     "cie_paged_fwd",
+    "cie_paged_fwd_noalloc",
     "cie_kv_append",
     "cie_rope_apply",
     "cie_flash_fwd_rope",
@@ -73,6 +74,9 @@ def _declare(lib: ctypes.CDLL) -> None:
                                   _i, _i, _i, _i, _i, _i, _i, _i, _i,
                                   ctypes.c_float, _i, _i, _vp]
     lib.cie_paged_fwd.restype = _i
+    lib.cie_paged_fwd_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
+                                          _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp]
+    lib.cie_paged_fwd_noalloc.restype = _i
     lib.cie_kv_append.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]
     lib.cie_kv_append.restype = _i

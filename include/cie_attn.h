@@ -125,6 +125,27 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
                   void* stream);
 
 /*
+ * cie_paged_fwd without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture that must not call the
+ * allocator, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments, semantics and results as
+ * cie_paged_fwd, bit for bit; the workspace is a static 16 MiB device array
+ * of the library (one per GPU, held until the process ends), so this entry
+ * allocates and frees nothing. A shape whose cie_paged_workspace_bytes
+ * exceeds 16 MiB is rejected with CIE_EWORKSPACE before any HIP call.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (concurrent streams, threads) race and must be serialised by the caller.
+ */
+int cie_paged_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, const int32_t* context_lens, void* o,
+                          const int64_t* q_stride, const int64_t* kc_stride,
+                          const int64_t* vc_stride, const int64_t* o_stride,
+                          int B, int Hq, int Hk, int Lq, int D,
+                          int num_blocks, int block_size, int max_blocks_per_seq,
+                          int max_context, float scale, int causal, int dtype,
+                          void* stream);
+
+/*
  * Paged KV append: writes the new tokens of B sequences into the pool.
  *   k_new, v_new: (T, Hk, D) rows; the rows of sequence b are
  *        cu_new[b] .. cu_new[b+1]-1 (int32 [B+1], cu_new[0] = 0, cu_new[B] = T)
