@@ -135,11 +135,16 @@ class FlashLaunch:
 
 
 class PagedLaunch:
-    """Pre-bound cie_paged_fwd call rotating over `copies` KV pool copies."""
+    """Pre-bound paged attention call rotating over `copies` KV pool copies:
+    cie_paged_fwd (schedule derived on the device from the lengths), or with
+    `planned` cie_paged_fwd_ex reading a work plan built on the host from the
+    same lengths and block tables and uploaded beforehand, as an engine step
+    does once for all its layers."""
 
-    def __init__(self, case, dev, min_bytes=512 << 20):
+    def __init__(self, case, dev, min_bytes=512 << 20, planned=False):
         import torch
         from engine import _lib
+        from engine.attention import paged_plan
 
         self.lib = _lib.load()
         self.q = case.q.to(dev)
@@ -156,10 +161,19 @@ class PagedLaunch:
         ws = self.lib.cie_paged_workspace_bytes(B, Hq, Hk, Lq, D, mc, bs, mb)
         self.ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
         self._keep = [_lib.strides(t) for t in (self.q, self.pools[0][0], self.pools[0][1], self.o)]
-        self.head = (self.q.data_ptr(),)
-        self.tail = (self.bt.data_ptr(), self.lens.data_ptr(), self.o.data_ptr(), self.ws.data_ptr(), ws,
-                     *self._keep, B, Hq, Hk, Lq, D, nb, bs, mb, mc, ctypes.c_float(1.0 / math.sqrt(D)), 1,
-                     _lib.DTYPE_CODES[self.q.dtype])
+        self.planned = planned
+        if planned:
+            self.plan = paged_plan(case.context_lens, case.block_tables, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb,
+                                   block_size=bs, max_context=mc, device=dev)
+            self._none3 = (ctypes.c_int64 * 3)(0, 0, 1)
+            self.tail = (None, None, self.plan.data.data_ptr(), self.plan.split, self.o.data_ptr(),
+                         self.ws.data_ptr(), ws, self._keep[0], self._none3, self._none3, *self._keep[1:],
+                         B, Hq, Hk, Lq, D, nb, bs, mb, mc, ctypes.c_float(1.0 / math.sqrt(D)), 1,
+                         _lib.DTYPE_CODES[self.q.dtype], None, None, 0, 0)
+        else:
+            self.tail = (self.bt.data_ptr(), self.lens.data_ptr(), self.o.data_ptr(), self.ws.data_ptr(), ws,
+                         *self._keep, B, Hq, Hk, Lq, D, nb, bs, mb, mc, ctypes.c_float(1.0 / math.sqrt(D)), 1,
+                         _lib.DTYPE_CODES[self.q.dtype])
         self.dev = dev
         self.ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in self.pools]
         self.bytes = case.bytes
@@ -167,7 +181,10 @@ class PagedLaunch:
 
     def __call__(self, i=0):
         kp, vp = self.ptrs[i % self.copies]
-        rc = self.lib.cie_paged_fwd(self.q.data_ptr(), kp, vp, *self.tail, _stream(self.dev))
+        if self.planned:
+            rc = self.lib.cie_paged_fwd_ex(self.q.data_ptr(), None, None, kp, vp, *self.tail, _stream(self.dev))
+        else:
+            rc = self.lib.cie_paged_fwd(self.q.data_ptr(), kp, vp, *self.tail, _stream(self.dev))
         if rc:
             from engine import _lib
             _lib.check(rc)
@@ -494,26 +511,68 @@ def event_time_ms(fn, n, warmup, trials=3):
     return statistics.median(res)
 
 
-def cpu_baseline(case):
-    """The reference's algorithm (fp32 up-cast, repeat_interleave GQA, full
-    score matrix, bottom-right mask, softmax, PV) on the host cores."""
-    import torch
-    from oracle import flash_attention_ref
-
-    cores = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(cores)
-    q, k, v = case.q.float(), case.k.float(), case.v.float()
-    flash_attention_ref(q[:1, :8], k[:1, :2], v[:1, :2], causal=True)  # warm-up
+def _timed(fn, runs):
+    """fn() once untimed, then the median wall time of `runs` calls."""
+    fn()
     times = []
-    for _ in range(3):
+    for _ in range(runs):
         t0 = time.perf_counter()
-        flash_attention_ref(q, k, v, causal=True)
+        fn()
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": round(case.flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"full {case.name} workload through the fp32 oracle (unchunked: 4x32x2048x2048 "
-                      f"score matrix), median of 3 runs, {t:.2f} s each"}
+    return statistics.median(times)
+
+
+def cpu_baselines(names=("prefill_s128", "prefill_s2048", "decode_b32", "verify_b8", "prefill_s16384")):
+    """The reference's CPU path (kernels/ref/flash_attention_ref.py:8-56: fp32
+    up-cast, repeat_interleave GQA, full score matrix, bottom-right mask,
+    softmax, P.V), restated by the oracle, on every host core this process may
+    use, for each workload: the prefill cases as one call over the whole
+    batch (the S=16384 case chunked over query blocks, on a bounded sample),
+    the paged cases per sequence as the reference's engine runs them
+    (engine/model/block.py:56-71: gather the history through the block
+    table, then attend). Each figure is in its workload's GPU unit (TFLOP/s
+    of algorithmic work, or GB/s of algorithmic bytes)."""
+    import torch
+    from benchmarks import workloads
+    from oracle import flash_attention_ref, flash_attention_ref_chunked, gather_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = {}
+    for name in names:
+        c = workloads.WORKLOADS[name]()
+        if name.startswith("prefill"):
+            q, k, v = c.q.float(), c.k.float(), c.v.float()
+            if name == "prefill_s16384":
+                # bounded sample: batch 0, kv head 0 with its 4 query heads (1/8 of the work), every
+                # query row, chunked over 2048-row query blocks (the full score matrix is 34 GB)
+                qs, ks, vs = q[:, :4], k[:, :1], v[:, :1]
+                t = _timed(lambda: flash_attention_ref_chunked(qs, ks, vs, causal=True, q_chunk=2048), 1)
+                flops = c.flops / 8
+                sample = (f"kv head 0 with its 4 query heads over all 16384 rows (1/8 of the workload), "
+                          f"fp32 oracle chunked over 2048-row query blocks, 1 run, {t:.2f} s")
+            else:
+                t = _timed(lambda: flash_attention_ref(q, k, v, causal=True), 3)
+                flops = c.flops
+                sample = f"full {name} workload through the unchunked fp32 oracle, median of 3 runs, {t:.3f} s each"
+            out[name] = {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+                         "kind": "port", "sample": sample}
+        else:
+            B, Hq, Lq, D = c.q.shape
+            lens = c.context_lens.tolist()
+
+            def per_sequence():
+                for b in range(B):
+                    kd = gather_ref(c.k_pool, c.block_tables[b], lens[b]).float().transpose(0, 1).unsqueeze(0)
+                    vd = gather_ref(c.v_pool, c.block_tables[b], lens[b]).float().transpose(0, 1).unsqueeze(0)
+                    flash_attention_ref(c.q[b:b + 1].float(), kd, vd, causal=True)
+
+            t = _timed(per_sequence, 3)
+            out[name] = {"value": round(c.bytes / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+                         "kind": "port",
+                         "sample": f"full {name} workload, per sequence: gather through the block table, then "
+                                   f"the fp32 oracle with Lq={Lq}; median of 3 runs, {t:.3f} s each"}
+    return out
 
 
 def main():
@@ -562,13 +621,23 @@ def main():
     if not args.no_extra:
         for name in ("decode_b32", "verify_b8"):
             c = workloads.WORKLOADS[name]()
-            pl = PagedLaunch(c, dev)
+            # with the host-built plan (what an engine step uses, uploaded once for all layers) and
+            # with the schedule derived on the device from the lengths alone
+            pl = PagedLaunch(c, dev, planned=True)
             ms = event_time_ms(pl, 40 * pl.copies, 2 * pl.copies)
             gbs = c.bytes / (ms / 1e3) / 1e9
-            extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
-                           "bytes": int(c.bytes), "pool_copies": pl.copies,
-                           "dtype": "fp16" if c.q.dtype == torch.float16 else "bf16"}
+            split = pl.plan.split
             del pl
+            pd = PagedLaunch(c, dev)
+            ms_dev = event_time_ms(pd, 40 * pd.copies, 2 * pd.copies)
+            gbs_dev = c.bytes / (ms_dev / 1e3) / 1e9
+            extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
+                           "schedule": "host plan", "split_sequences": split,
+                           "device_schedule": {"GB/s": round(gbs_dev, 1), "frac_hbm": round(gbs_dev / PEAK_HBM_GBS, 4),
+                                               "us": round(ms_dev * 1e3, 2)},
+                           "bytes": int(c.bytes), "pool_copies": pd.copies,
+                           "dtype": "fp16" if c.q.dtype == torch.float16 else "bf16"}
+            del pd
         for name, (B, L) in (("append_prefill_b4_l2048", (4, 2048)), ("append_decode_b32", (32, 1))):
             al = AppendLaunch(B, L, dev)
             ms = graph_time_ms(al, n_inner=max(20, al.copies))
@@ -602,9 +671,23 @@ def main():
         extra["prefill_s16384"] = {"TFLOP/s": round(t5, 2), "frac_mfma": round(t5 / PEAK_MFMA_F16_TFLOPS, 4),
                                    "us": round(ms * 1e3, 1), "dtype": "bf16"}
         del f5
+        # the CPU-oracle case (fp32 on the host) run on the GPU with its tensors cast to fp16
+        c1 = workloads.prefill_s128(dtype=torch.float16)
+        f1 = FlashLaunch(c1, dev)
+        ms = graph_time_ms(f1, n_inner=20)
+        t1 = c1.flops / (ms / 1e3) / 1e12
+        extra["prefill_s128"] = {"TFLOP/s": round(t1, 3), "frac_mfma": round(t1 / PEAK_MFMA_F16_TFLOPS, 5),
+                                 "us": round(ms * 1e3, 2), "dtype": "fp16", "timing": "graph replay",
+                                 "note": "32 workgroups: latency-bound, far too small to fill 256 CUs"}
+        del f1
         torch.cuda.empty_cache()
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(case)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpus = cpu_baselines() if not args.no_extra else cpu_baselines(("prefill_s2048",))
+        cpu = cpus.pop("prefill_s2048")
+        for name, base in cpus.items():
+            extra.setdefault(name, {})["cpu_baseline"] = base
 
     line = {
         "metric": "prefill attention TFLOP/s + paged-decode KV GB/s (% roofline) on 1 MI355X",

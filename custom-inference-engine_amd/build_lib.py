@@ -22,7 +22,8 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libcie_attn.so")
 
-SOURCES = ["capi.cpp", "flash_fwd.hip", "paged_fwd.hip", "kv_append.hip", "rope.hip", "int8_gemm.hip"]
+SOURCES = ["capi.cpp", "paged_plan.cpp", "flash_fwd.hip", "paged_fwd.hip", "kv_append.hip", "rope.hip",
+           "int8_gemm.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 COMMON = [

@@ -208,6 +208,41 @@ size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D, int max_c
   return g.ok ? g.info_bytes + g.slot_bytes : 0;
 }
 
+size_t cie_paged_plan_bytes(int B, int Hq, int Hk, int Lq, int D, int max_context, int block_size,
+                            int max_blocks_per_seq) {
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Lq <= 0 || D <= 0 || block_size <= 0 || max_blocks_per_seq < 0 ||
+      Hq % Hk)
+    return 0;
+  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff) return 0;
+  const cie::PagedGeom g =
+      cie::paged_geometry(B, Hq, Hk, Lq, D, paged_ctx_limit(max_context, block_size, max_blocks_per_seq), block_size);
+  if (!g.ok) return 0;
+  const cie::PlanLayout L = cie::paged_plan_layout(g, B, max_blocks_per_seq);
+  if (L.ints > 0x7fffffff) return 0;
+  return L.ints * sizeof(int32_t);
+}
+
+int cie_paged_plan(void* plan, size_t plan_bytes, const int32_t* context_lens, const int32_t* block_tables,
+                   int64_t block_table_row_stride, int B, int Hq, int Hk, int Lq, int D, int num_blocks,
+                   int block_size, int max_blocks_per_seq, int max_context, int for_append) {
+  if (!plan || !context_lens || (!block_tables && B > 0)) return fail(CIE_EINVAL, "plan: NULL pointer");
+  if (num_blocks < 0 || block_table_row_stride < max_blocks_per_seq)
+    return fail(CIE_EINVAL, "plan: block table row stride %lld is below max_blocks_per_seq %d",
+                (long long)block_table_row_stride, max_blocks_per_seq);
+  const size_t need = cie_paged_plan_bytes(B, Hq, Hk, Lq, D, max_context, block_size, max_blocks_per_seq);
+  if (need == 0) return fail(CIE_EINVAL, "plan: unsupported shape");
+  if (plan_bytes < need) return fail(CIE_EWORKSPACE, "plan: %zu bytes required, %zu given", need, plan_bytes);
+  const int ctx_limit = paged_ctx_limit(max_context, block_size, max_blocks_per_seq);
+  const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size);
+  const cie::PlanLayout L = cie::paged_plan_layout(g, B, max_blocks_per_seq);
+  const int split = cie::build_paged_plan(static_cast<int32_t*>(plan), g, L, context_lens, block_tables,
+                                          block_table_row_stride, B, Lq, num_blocks, block_size,
+                                          max_blocks_per_seq, ctx_limit, for_append ? 1 : 0);
+  if (split < 0) return fail(CIE_EINVAL, "plan: a range exceeds the launch geometry");
+  g_err.clear();
+  return split;
+}
+
 }  // extern "C"
 
 static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
@@ -220,7 +255,8 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
                       int max_context, float scale, int causal, int dtype,
                       void* stream, cie::RopeTables rope,
                       const void* k_new = nullptr, const void* v_new = nullptr,
-                      const int64_t* kn_stride = nullptr, const int64_t* vn_stride = nullptr) {
+                      const int64_t* kn_stride = nullptr, const int64_t* vn_stride = nullptr,
+                      const void* plan = nullptr, int plan_split = -1) {
   CIE_TRY(common_checks(Hq, Hk, D, dtype));
   if (B < 0 || Lq < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d)", B, Lq);
   if (block_size < 1) return fail(CIE_EINVAL, "block_size must be positive, got %d", block_size);
@@ -238,7 +274,12 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   CIE_TRY(check_ptr("o", o));
   CIE_TRY(check_ptr("k_cache", k_cache));
   CIE_TRY(check_ptr("v_cache", v_cache));
-  if (!block_tables || !context_lens) return fail(CIE_EINVAL, "block_tables / context_lens: NULL pointer");
+  if (plan) {
+    CIE_TRY(check_ptr("plan", plan));
+    if (plan_split < 0) return fail(CIE_EINVAL, "plan_split must be the count cie_paged_plan returned");
+  } else if (!block_tables || !context_lens) {
+    return fail(CIE_EINVAL, "block_tables / context_lens: NULL pointer");
+  }
   CIE_TRY(check_strides("q", q_stride));
   CIE_TRY(check_strides("o", o_stride));
   CIE_TRY(check_strides("k_cache", kc_stride));
@@ -256,11 +297,16 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   if ((int64_t)B * ((ctx_limit + 31) / 32) > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
   const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size);
   if (!g.ok) return fail(CIE_EINVAL, "paged attention: %s", g.err);
-  const size_t need = g.info_bytes + g.slot_bytes;
-  if (!workspace || workspace_bytes < need)
-    return fail(CIE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
-                workspace ? workspace_bytes : (size_t)0);
-  if (!aligned16(workspace)) return fail(CIE_EINVAL, "workspace: pointer is not 16-byte aligned");
+  // with a plan the piece descriptors live in the plan; the workspace holds
+  // only the partial states, and none at all when no sequence is split
+  const bool merge = !plan || plan_split > 0;
+  const size_t need = plan ? (merge ? g.slot_bytes : 0) : g.info_bytes + g.slot_bytes;
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(CIE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(CIE_EINVAL, "workspace: pointer is not 16-byte aligned");
+  }
 
   cie::PagedParams p{};
   p.q = static_cast<const uint16_t*>(q);
@@ -269,8 +315,19 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   p.o = static_cast<uint16_t*>(o);
   p.bt = block_tables;
   p.lens = context_lens;
-  p.info = static_cast<int4*>(workspace);
-  p.slots = reinterpret_cast<float*>(static_cast<char*>(workspace) + g.info_bytes);
+  if (plan) {
+    const cie::PlanLayout L = cie::paged_plan_layout(g, B, max_blocks_per_seq);
+    p.plan = static_cast<const int32_t*>(plan);
+    p.plan_ranges = (int)L.ranges;
+    p.plan_entries = (int)L.entries;
+    p.plan_ids = (int)L.ids;
+    p.plan_empty = (int)L.empty;
+    p.info = const_cast<int4*>(reinterpret_cast<const int4*>(p.plan + L.info));  // read only in this mode
+    p.slots = static_cast<float*>(workspace);
+  } else {
+    p.info = static_cast<int4*>(workspace);
+    p.slots = reinterpret_cast<float*>(static_cast<char*>(workspace) + g.info_bytes);
+  }
   p.qs0 = q_stride[0]; p.qs1 = q_stride[1]; p.qs2 = q_stride[2];
   p.ks0 = kc_stride[0]; p.ks1 = kc_stride[1]; p.ks2 = kc_stride[2];
   p.vs0 = vc_stride[0]; p.vs1 = vc_stride[1]; p.vs2 = vc_stride[2];
@@ -309,7 +366,7 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
     p.kns0 = kn_stride[0]; p.kns1 = kn_stride[1];
     p.vns0 = vn_stride[0]; p.vns1 = vn_stride[1];
   }
-  return launch_status(cie::launch_paged(p, dtype, D, g.lds_bytes, static_cast<hipStream_t>(stream)));
+  return launch_status(cie::launch_paged(p, dtype, D, g.lds_bytes, merge, static_cast<hipStream_t>(stream)));
 }
 
 extern "C" {
@@ -326,6 +383,28 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
   return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
                     kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
                     max_context, scale, causal, dtype, stream, cie::RopeTables{nullptr, nullptr, 0, 0});
+}
+
+int cie_paged_fwd_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                     const int32_t* block_tables, const int32_t* context_lens, const void* plan, int plan_split,
+                     void* o, void* workspace, size_t workspace_bytes,
+                     const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
+                     const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,
+                     int B, int Hq, int Hk, int Lq, int D,
+                     int num_blocks, int block_size, int max_blocks_per_seq,
+                     int max_context, float scale, int causal, int dtype,
+                     const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
+                     void* stream) {
+  if ((k_new == nullptr) != (v_new == nullptr)) return fail(CIE_EINVAL, "k_new / v_new: give both or neither");
+  cie::RopeTables rope{nullptr, nullptr, 0, 0};
+  if (rope_cos || rope_sin) {
+    CIE_TRY(check_rope(rope_cos, rope_sin, rope_rows, rope_dtype));
+    rope = cie::RopeTables{rope_cos, rope_sin, rope_rows, rope_dtype};
+  }
+  return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
+                    kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
+                    max_context, scale, causal, dtype, stream, rope, k_new, v_new, kn_stride, vn_stride, plan,
+                    plan ? plan_split : -1);
 }
 
 int cie_paged_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,

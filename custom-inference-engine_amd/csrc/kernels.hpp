@@ -80,6 +80,10 @@ struct PagedParams {
   const uint16_t* kn;
   const uint16_t* vn;
   int64_t kns0, kns1, vns0, vns1;
+  // Host-built plan (paged_plan.cpp), or nullptr: the schedule is then
+  // derived on the device from lens and bt. Offsets in int32 elements.
+  const int32_t* plan;
+  int plan_ranges, plan_entries, plan_ids, plan_empty;
 };
 
 constexpr int kPagedTile = 32;         // tokens per tile
@@ -103,6 +107,22 @@ struct PagedGeom {
   size_t info_bytes, slot_bytes;  // workspace parts
 };
 PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size);
+
+// Host-built plan of a paged launch (see paged_plan.cpp for the layout).
+constexpr int32_t kPlanMagic = 0x43504c31;  // "CPL1"
+constexpr int kPlanHeader = 16;             // header ints
+constexpr int kPlanRangeInts = 8;           // ints per range row
+struct PlanLayout {
+  size_t ranges, entries, ids, info, empty;  // section offsets (int32 elements)
+  size_t ints;                               // total size
+};
+PlanLayout paged_plan_layout(const PagedGeom& g, int B, int max_blocks);
+// Fills P (layout L) from host lengths and block tables; returns the number
+// of sequences split across workgroups (>= 0), or -1 when the geometry's
+// bounds are violated.
+int build_paged_plan(int32_t* P, const PagedGeom& g, const PlanLayout& L, const int32_t* lens,
+                     const int32_t* bt, int64_t bt_stride, int B, int Lq, int num_blocks, int block_size,
+                     int max_blocks, int ctx_limit, int append);
 
 // Paged KV append: new token rows (T, Hk, D) into the pool through block tables.
 struct AppendParams {
@@ -185,7 +205,9 @@ hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stre
 hipError_t launch_int8_gemm(const I8GemmParams& p, const I8Geom& g, int dtype, hipStream_t stream);
 hipError_t launch_kv_append(const AppendParams& p, int B, int max_new, int dtype, int D, hipStream_t stream);
 hipError_t launch_rope(const RopeParams& p, int dtype, int D, hipStream_t stream);
-hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, hipStream_t stream);
+// merge: launch the merge pass of split sequences (false only when a plan
+// says no sequence is split)
+hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds_bytes, bool merge, hipStream_t stream);
 
 // Bytes of the static device workspace behind cie_paged_fwd_noalloc.
 constexpr size_t kPagedScratchBytes = (size_t)16 << 20;

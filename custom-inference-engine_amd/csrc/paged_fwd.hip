@@ -88,6 +88,13 @@ __device__ __forceinline__ int div_small(uint64_t n, uint32_t d) {
   return n <= 0xffffffffull ? (int)((uint32_t)n / d) : (int)(n / d);
 }
 
+// The plan header names this launch: magic, range count, batch and whether
+// it was built for the fused append.
+__device__ __forceinline__ bool plan_matches(const PagedParams& p) {
+  const int32_t* P = p.plan;
+  return P[0] == kPlanMagic && P[3] == p.Wg && P[6] == p.B && P[7] == (p.kn ? 1 : 0);
+}
+
 __device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
   // with a fused append the Lq new tokens are part of every valid context
   return ctx >= (p.kn ? p.Lq : 0) && ctx <= p.ctx_limit && (ctx == 0 || p.num_blocks > 0);
@@ -167,6 +174,43 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   const int hq = kvh * p.group + g;
   const uint32_t nan2 = 0x7fff7fffu;  // NaN in both fp16 and bf16
 
+  const uint32_t sbt_lds = lds_addr_of(sbt);
+  int ne = 0, nid = 0, S0 = 0, T = 0;
+  if (p.plan) {
+    // ---- schedule from the host-built plan: this range's row, then its
+    // entries and block ids (already validated) copied straight into LDS ----
+    const int32_t* P = p.plan;
+    const bool ok = plan_matches(p);
+    const int32_t* row = P + p.plan_ranges + kPlanRangeInts * j;
+    if (ok) {
+      ne = min(row[1], kPagedEntries);
+      nid = min(row[3], kPagedIds);
+      S0 = row[4];
+      T = row[5];
+    }
+    if (j == 0) {
+      // sequences without tiles (zeros for an empty history, NaN for an
+      // invalid length); every sequence NaN when the plan is not this launch's
+      const int nz = ok ? min(P[4], p.B) : p.B;
+      const int32_t* Z = P + p.plan_empty;
+      for (int z = 0; z < nz; ++z) {
+        const int bz = ok ? Z[2 * z] : z;
+        const bool zvalid = ok && Z[2 * z + 1] != 0;
+        if (rv && (uint32_t)bz < (uint32_t)p.B)
+          fill_row_half<D>(p.o + (int64_t)bz * p.os0 + hq * p.os1 + (int64_t)i * p.os2, hl, zvalid ? 0u : nan2);
+      }
+    }
+    if (w == 0 && T > 0) {
+      const int32_t* es = P + p.plan_entries + 8 * row[0];
+      const uint32_t ent_lds = lds_addr_of(ent);
+      for (int x0 = 0; x0 < 8 * ne; x0 += 64)
+        if (x0 + lane < 8 * ne) dma4(es + x0 + lane, ent_lds + 4u * (uint32_t)x0);
+      const int32_t* is = P + p.plan_ids + row[2];
+      for (int x0 = 0; x0 < nid; x0 += 64)
+        if (x0 + lane < nid) dma4(is + x0 + lane, sbt_lds + 4u * (uint32_t)x0);
+      vm_wait<0>();
+    }
+  } else {
   // ---- schedule: every wave derives it from the context lengths ----------
   // ctx0, incl0: this lane's length and inclusive tile prefix among the
   // first 64 sequences, reused below
@@ -181,10 +225,10 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   // W <= NT ranges, so none is empty: every range a sequence spans holds one
   // of its pieces (workgroups j >= W have nothing to do).
   const int W = min(p.Wg, NT);
-  const int S0 = j < W ? div_small((uint64_t)j * (uint32_t)NT, (uint32_t)W) : NT;
+  S0 = j < W ? div_small((uint64_t)j * (uint32_t)NT, (uint32_t)W) : NT;
   const int S1 = j < W ? div_small((uint64_t)(j + 1) * (uint32_t)NT, (uint32_t)W) : NT;
 
-  int ne = 0, nid = 0, carry = 0;
+  int carry = 0;
   for (int b0 = 0; b0 < p.B; b0 += 64) {
     if (j != 0 && carry >= S1) break;
     const int b = b0 + lane;
@@ -238,11 +282,10 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     ne += __builtin_popcountll(om);
     nid += __builtin_amdgcn_readlane(ids_incl, 63);
   }
-  const int T = S1 - S0;
+  T = S1 - S0;
 
   // Stage the block ids of the range in LDS (one direct-to-LDS dword per id);
   // ids outside [0, num_blocks) become -1 (never dereferenced, poison the piece).
-  const uint32_t sbt_lds = lds_addr_of(sbt);
   if (w == 0 && T > 0) {
     for (int e = 0; e < ne; ++e) {
       // entry fields are wave-uniform; readfirstlane keeps the address math scalar
@@ -261,6 +304,7 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     for (int x = lane; x < nid; x += 64)
       if ((uint32_t)sbt[x] >= (uint32_t)p.num_blocks) sbt[x] = -1;
   }
+  }  // device-derived schedule
   __syncthreads();
   if (T == 0) return;
 
@@ -558,8 +602,10 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
 
     if (n == c_end - 1) {  // last tile of the piece
       const float l_tot = xhalf_sum(l);
-      if (ent[ce][7] == 1) {
-        const float inv = poison ? __builtin_nanf("") : 1.f / l_tot;
+      if (ent[ce][7] == 1 || !p.slots) {
+        // (no partial-state space: the caller's plan said nothing is split,
+        // which this plan contradicts; the rows are NaN rather than partial)
+        const float inv = poison || ent[ce][7] != 1 ? __builtin_nanf("") : 1.f / l_tot;
         if (rv) store_row<DTYPE, D>(p.o + (int64_t)c_b * p.os0 + hq * p.os1 + (int64_t)i * p.os2, acc, inv, hl);
       } else {
         // Piece of a split sequence: side 1 if it starts inside this range.
@@ -714,7 +760,10 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   const int pieces = inf.y;
   const int hh = w % p.Hg, qt = w / p.Hg;
   const int r = qt * 32 + row;
-  const bool act = in && pieces > 1 && r < p.R;
+  // a descriptor that does not name ranges of this launch (a plan built for
+  // other arguments) is ignored: the main pass has written NaN rows then
+  const bool described = inf.x >= 0 && pieces <= p.Wg && inf.x <= p.Wg - pieces && (!p.plan || plan_matches(p));
+  const bool act = in && pieces > 1 && r < p.R && described;
   const int64_t slot_floats = (int64_t)p.Rt * (D + 2);
 
   float M = -INFINITY, L = 0.f;
@@ -804,7 +853,7 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
 }
 
 template <int DTYPE, int D>
-static hipError_t launch_paged_t(const PagedParams& p, size_t lds, hipStream_t stream) {
+static hipError_t launch_paged_t(const PagedParams& p, size_t lds, bool merge, hipStream_t stream) {
   const void* fn = p.kn ? reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D, true>)
                         : reinterpret_cast<const void*>(&paged_fwd_kernel<DTYPE, D, false>);
   const hipError_t attr = set_dynamic_lds(fn, kPagedLdsBudget);
@@ -815,26 +864,26 @@ static hipError_t launch_paged_t(const PagedParams& p, size_t lds, hipStream_t s
   else
     hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D, false>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !merge) return e;
   const int64_t threads = (int64_t)p.B * p.NG * p.NWV * p.Rt * (D / 4) * kMergeLanes;
   hipLaunchKernelGGL((paged_merge_kernel<DTYPE, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 template <int DTYPE>
-static hipError_t launch_paged_d(const PagedParams& p, int D, size_t lds, hipStream_t stream) {
+static hipError_t launch_paged_d(const PagedParams& p, int D, size_t lds, bool merge, hipStream_t stream) {
   switch (D) {
-    case 16: return launch_paged_t<DTYPE, 16>(p, lds, stream);
-    case 32: return launch_paged_t<DTYPE, 32>(p, lds, stream);
-    case 64: return launch_paged_t<DTYPE, 64>(p, lds, stream);
-    case 128: return launch_paged_t<DTYPE, 128>(p, lds, stream);
-    case 256: return launch_paged_t<DTYPE, 256>(p, lds, stream);
+    case 16: return launch_paged_t<DTYPE, 16>(p, lds, merge, stream);
+    case 32: return launch_paged_t<DTYPE, 32>(p, lds, merge, stream);
+    case 64: return launch_paged_t<DTYPE, 64>(p, lds, merge, stream);
+    case 128: return launch_paged_t<DTYPE, 128>(p, lds, merge, stream);
+    case 256: return launch_paged_t<DTYPE, 256>(p, lds, merge, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds, hipStream_t stream) {
-  return dtype == 0 ? launch_paged_d<0>(p, D, lds, stream) : launch_paged_d<1>(p, D, lds, stream);
+hipError_t launch_paged(const PagedParams& p, int dtype, int D, size_t lds, bool merge, hipStream_t stream) {
+  return dtype == 0 ? launch_paged_d<0>(p, D, lds, merge, stream) : launch_paged_d<1>(p, D, lds, merge, stream);
 }
 
 // Static workspace of the allocation-free paged entry: one copy per GPU,

@@ -35,6 +35,9 @@ EXPORTED_SYMBOLS = (
     "cie_paged_workspace_bytes",
     "cie_paged_fwd",
     "cie_paged_fwd_noalloc",
+    "cie_paged_plan_bytes",
+    "cie_paged_plan",
+    "cie_paged_fwd_ex",
     "cie_kv_append",
     "cie_rope_apply",
     "cie_flash_fwd_rope",
@@ -77,6 +80,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cie_paged_fwd_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
                                           _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp]
     lib.cie_paged_fwd_noalloc.restype = _i
+    lib.cie_paged_plan_bytes.argtypes = [_i, _i, _i, _i, _i, _i, _i, _i]
+    lib.cie_paged_plan_bytes.restype = ctypes.c_size_t
+    lib.cie_paged_plan.argtypes = [_vp, ctypes.c_size_t, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _i, _i, _i, _i,
+                                   _i, _i]
+    lib.cie_paged_plan.restype = _i
+    lib.cie_paged_fwd_ex.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, ctypes.c_size_t,
+                                     _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
+                                     _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i,
+                                     _vp, _vp, _i, _i, _vp]
+    lib.cie_paged_fwd_ex.restype = _i
     lib.cie_kv_append.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p, _vp, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]
     lib.cie_kv_append.restype = _i

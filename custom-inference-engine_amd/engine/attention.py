@@ -13,7 +13,9 @@ Both accept fp16 and bf16 (the reference accepts fp16 only,
 
 from __future__ import annotations
 
+import ctypes
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -152,6 +154,66 @@ def flash_attention(
     return out
 
 
+@dataclass(frozen=True)
+class PagedPlan:
+    """A host-built work plan of paged attention (``cie_paged_plan``): the
+    share of every workgroup, the block ids it reads and the piece
+    descriptors of the merge pass, for one launch shape and one set of
+    context lengths and block tables. ``data`` is the int32 plan (on the
+    device for a launch), ``split`` the number of sequences split across
+    workgroups, ``key`` the launch shape it was built for."""
+    data: torch.Tensor
+    split: int
+    key: tuple
+
+
+def paged_plan_ints(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size: int, max_blocks_per_seq: int,
+                    max_context: int | None = None) -> int:
+    """int32 elements of a plan for this launch shape (0 if unsupported)."""
+    return int(_lib.load().cie_paged_plan_bytes(B, Hq, Hk, Lq, D, int(max_context or 0), block_size,
+                                                max_blocks_per_seq)) // 4
+
+
+def paged_plan_fill(out: torch.Tensor, context_lens: torch.Tensor, block_tables: torch.Tensor, *, Hq: int,
+                    Hk: int, Lq: int, D: int, num_blocks: int, block_size: int, max_context: int | None = None,
+                    for_append: bool = False) -> tuple[int, tuple]:
+    """Fill ``out`` (a contiguous host int32 tensor of at least
+    :func:`paged_plan_ints` elements) with the plan of a launch over host
+    ``context_lens`` (B,) and ``block_tables`` (B, max_blocks), int32.
+    Returns (split sequences, key)."""
+    B, max_blocks = block_tables.shape
+    lens = context_lens.to(torch.int32).contiguous()
+    bt = block_tables.to(torch.int32).contiguous()
+    if lens.is_cuda or bt.is_cuda or out.is_cuda:
+        raise ValueError("paged plans are built from host tensors")
+    if lens.shape != (B,) or out.dtype != torch.int32 or not out.is_contiguous():
+        raise ValueError("paged_plan_fill: context_lens must be (B,) and out a contiguous int32 tensor")
+    mc = int(max_context or 0)
+    rc = _lib.load().cie_paged_plan(out.data_ptr(), out.numel() * 4, lens.data_ptr(), bt.data_ptr(),
+                                    bt.stride(0), B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc,
+                                    1 if for_append else 0)
+    if rc < 0:
+        _lib.check(rc)
+    return rc, (B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc, bool(for_append))
+
+
+def paged_plan(context_lens: torch.Tensor, block_tables: torch.Tensor, *, Hq: int, Hk: int, Lq: int, D: int,
+               num_blocks: int, block_size: int, max_context: int | None = None, for_append: bool = False,
+               device: torch.device | str = "cuda") -> PagedPlan:
+    """Build a plan on the host and copy it to ``device``. ``for_append``:
+    the plan is for a launch with ``new_kv`` (whose contexts must count
+    their Lq new tokens)."""
+    B, max_blocks = block_tables.shape
+    n = paged_plan_ints(B, Hq, Hk, Lq, D, block_size, max_blocks, max_context)
+    if n == 0:
+        raise ValueError("paged_plan: unsupported shape")
+    host = torch.empty(n, dtype=torch.int32)
+    split, key = paged_plan_fill(host, context_lens.cpu(), block_tables.cpu(), Hq=Hq, Hk=Hk, Lq=Lq, D=D,
+                                 num_blocks=num_blocks, block_size=block_size, max_context=max_context,
+                                 for_append=for_append)
+    return PagedPlan(host.to(device), split, key)
+
+
 def paged_workspace_bytes(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size: int,
                           max_blocks_per_seq: int, max_context: int | None = None) -> int:
     """Device workspace (bytes) a :func:`paged_attention` call of this shape
@@ -195,6 +257,7 @@ def paged_attention(
     rope: tuple[torch.Tensor, torch.Tensor] | None = None,
     out: torch.Tensor | None = None,
     new_kv: tuple[torch.Tensor, torch.Tensor] | None = None,
+    plan: PagedPlan | None = None,
 ) -> torch.Tensor:
     """Attention of the newest ``Lq`` tokens of each sequence over its paged
     KV history.
@@ -226,6 +289,12 @@ def paged_attention(
     must count its Lq new tokens (a shorter one gives NaN rows). With
     ``rope`` k_new is un-rotated too and is rotated at those positions, as
     ``kv_append(rope=)`` would (``cie_paged_fwd_append_rope``).
+
+    ``plan``: a :class:`PagedPlan` built on the host for exactly these
+    lengths, block tables and shape (:func:`paged_plan`, or
+    ``PagedKVCache.prepare_step``); the launch then reads every workgroup's
+    share of the work from it instead of deriving it on the device
+    (``cie_paged_fwd_ex``), with the same result bit for bit.
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_tables", block_tables), ("context_lens", context_lens)):
@@ -283,6 +352,22 @@ def paged_attention(
             _lib.strides(q), _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out),
             B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc,
             float(scale), 1 if causal else 0, _lib.DTYPE_CODES[q.dtype])
+    if plan is not None:
+        key = (B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks, mc, new_kv is not None)
+        if plan.key != key or not plan.data.is_cuda or plan.data.device != q.device:
+            raise ValueError(f"paged_attention: the plan was built for {plan.key}, this call is {key}")
+        none3 = (ctypes.c_int64 * 3)(0, 0, 1)
+        kn = (k_new.data_ptr(), v_new.data_ptr()) if new_kv is not None else (None, None)
+        kst = (_lib.strides3(k_new), _lib.strides3(v_new)) if new_kv is not None else (none3, none3)
+        rp = rope_args(rope, D, q.device) if rope is not None else (None, None, 0, 0)
+        with torch.cuda.device(q.device):
+            rc = lib.cie_paged_fwd_ex(q.data_ptr(), *kn, k_cache.data_ptr(), v_cache.data_ptr(), None, None,
+                                      plan.data.data_ptr(), plan.split, out.data_ptr(),
+                                      workspace.data_ptr() if plan.split else None, ws_have if plan.split else 0,
+                                      _lib.strides(q), *kst, _lib.strides(k_cache), _lib.strides(v_cache),
+                                      _lib.strides(out), *args[12:], *rp, stream)
+        _lib.check(rc)
+        return out
     with torch.cuda.device(q.device):
         if new_kv is not None:
             fargs = (q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),

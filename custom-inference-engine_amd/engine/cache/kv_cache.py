@@ -67,6 +67,14 @@ class StepBatch:
     tables: tuple = ()           # the host BlockTables, in batch order
     starts_host: tuple = ()      # host copies of starts and context lengths
     lengths_host: tuple = ()
+    plan: object = None          # engine.attention.PagedPlan of the step's paged launches, or None
+
+    def plan_for(self, append: bool):
+        """The step's paged-attention plan if it was built for a launch with
+        (``append``) or without the fused append, else None."""
+        if self.plan is not None and self.plan.key[-1] == append:
+            return self.plan
+        return None
 
     @property
     def fresh(self) -> bool:
@@ -262,14 +270,22 @@ class PagedKVCache:
         table.length = max(table.length, end)
 
     def prepare_step(self, tables: Sequence[BlockTable], num_new: int, starts: Sequence[int] | None = None,
-                     max_blocks: int | None = None) -> "StepBatch":
+                     max_blocks: int | None = None, *, num_heads: int | None = None,
+                     fused_append: bool | None = None) -> "StepBatch":
         """Host side of one engine step for a batch: allocate the blocks the
         ``num_new`` tokens of every sequence need (at ``starts[b]``, default
         each table's end), extend the lengths, and upload everything the
         step's kernels read (block tables, context lengths, the row offsets
         and start positions of the new tokens) in ONE host-to-device copy.
         Every layer's :meth:`append_step` and ``paged_attention`` of the step
-        reuses it, so no layer touches the host."""
+        reuses it, so no layer touches the host.
+
+        ``num_heads`` (the model's query heads): also build the work plan of
+        the step's paged attention launches on the host (``cie_paged_plan``)
+        and upload it in the same copy, so that no layer's launch derives
+        its schedule on the device. ``fused_append``: plan for the launch
+        with the append fused in (default: when the new tokens are the newest
+        of every sequence, the case ``attention_section`` fuses)."""
         if self.device.type != "cuda":
             raise RuntimeError("prepare_step requires a CUDA cache")
         starts = [t.length for t in tables] if starts is None else list(starts)
@@ -281,22 +297,46 @@ class PagedKVCache:
             t.length = max(t.length, s0 + num_new)
         B = len(tables)
         width = max([len(t.blocks) for t in tables] + [1]) if max_blocks is None else max_blocks
-        host = torch.zeros(B * width + 3 * B + 1, dtype=torch.int32)
+        lengths = tuple(t.length for t in tables)
+        max_context = max(lengths + (1,))
+        o = B * width
+        meta = o + 3 * B + 1
+        n_plan = 0
+        if num_heads is not None:
+            from engine.attention import paged_plan_ints
+
+            n_plan = paged_plan_ints(B, num_heads, self.cfg.num_kv_heads, num_new, self.cfg.head_dim,
+                                     self.cfg.block_size, width, max_context)
+        p0 = (meta + 3) // 4 * 4  # 16-byte aligned plan
+        host = torch.zeros(p0 + n_plan if n_plan else meta, dtype=torch.int32)
         for i, t in enumerate(tables):
             if len(t.blocks) > width:
                 raise ValueError(f"sequence {i} holds {len(t.blocks)} blocks, more than max_blocks={width}")
             if t.blocks:
                 host[i * width:i * width + len(t.blocks)] = torch.tensor(t.blocks, dtype=torch.int32)
-        o = B * width
-        host[o:o + B] = torch.tensor([t.length for t in tables], dtype=torch.int32)
+        host[o:o + B] = torch.tensor(lengths, dtype=torch.int32)
         host[o + B:o + 2 * B + 1] = torch.arange(B + 1, dtype=torch.int32) * num_new
-        host[o + 2 * B + 1:] = torch.tensor(starts, dtype=torch.int32)
+        host[o + 2 * B + 1:meta] = torch.tensor(starts, dtype=torch.int32)
+        split = key = None
+        if n_plan:
+            from engine.attention import paged_plan_fill
+
+            append = all(s0 + num_new == n for s0, n in zip(starts, lengths)) if fused_append is None \
+                else fused_append
+            split, key = paged_plan_fill(host[p0:p0 + n_plan], host[o:o + B], host[:o].view(B, width),
+                                         Hq=num_heads, Hk=self.cfg.num_kv_heads, Lq=num_new, D=self.cfg.head_dim,
+                                         num_blocks=self.cfg.num_blocks, block_size=self.cfg.block_size,
+                                         max_context=max_context, for_append=append)
         dev = host.to(self.device)
-        lengths = tuple(t.length for t in tables)
+        plan = None
+        if n_plan:
+            from engine.attention import PagedPlan
+
+            plan = PagedPlan(dev[p0:p0 + n_plan], split, key)
         return StepBatch(block_tables=dev[:o].view(B, width), context_lens=dev[o:o + B],
-                         cu_new=dev[o + B:o + 2 * B + 1], starts=dev[o + 2 * B + 1:], num_new=num_new,
-                         max_context=max(lengths + (1,)), tables=tuple(tables), starts_host=tuple(starts),
-                         lengths_host=lengths)
+                         cu_new=dev[o + B:o + 2 * B + 1], starts=dev[o + 2 * B + 1:meta], num_new=num_new,
+                         max_context=max_context, tables=tuple(tables), starts_host=tuple(starts),
+                         lengths_host=lengths, plan=plan)
 
     def append_step(self, layer: int, step: "StepBatch", k: torch.Tensor, v: torch.Tensor, *,
                     rope: tuple[torch.Tensor, torch.Tensor] | None = None,

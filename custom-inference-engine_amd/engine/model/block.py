@@ -81,7 +81,7 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
         cache._validate(v_rows)
         paged_attention(q, cache.k[layer_idx], cache.v[layer_idx], step.block_tables, step.context_lens,
                         causal=True, scale=scale, max_context=step.max_context, rope=rope, out=out,
-                        new_kv=(k_rows, v_rows))
+                        new_kv=(k_rows, v_rows), plan=step.plan_for(True))
     elif (Hq // Hk) * L <= _PAGED_MAX_ROWS:
         cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope)
         q_rope = rope
@@ -92,7 +92,8 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
             pos = step.starts[:, None] + torch.arange(L, device=q.device, dtype=torch.int32)[None, :]
             q, q_rope = rope_apply(q, rope[0], rope[1], positions=pos), None
         paged_attention(q, cache.k[layer_idx], cache.v[layer_idx], step.block_tables, step.context_lens,
-                        causal=True, scale=scale, max_context=step.max_context, rope=q_rope, out=out)
+                        causal=True, scale=scale, max_context=step.max_context, rope=q_rope, out=out,
+                        plan=step.plan_for(False))
     else:
         cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope)
         if rope is not None:

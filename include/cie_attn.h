@@ -125,6 +125,57 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
                   void* stream);
 
 /*
+ * Host-built work plan for paged attention (no reference counterpart: the
+ * reference never splits a context). Built once per engine step on the host
+ * from the host copies of the context lengths and block tables the step
+ * uploads anyway (BlockTable.blocks / .length, engine/cache/block_table.py:
+ * 16-18), copied to the device by the caller, and shared by every layer's
+ * launch of that step: the launch then reads each workgroup's share of the
+ * work directly instead of deriving it on the device from the lengths (three
+ * dependent memory round trips before the first KV tile).
+ *
+ * cie_paged_plan_bytes: host (and device) bytes of the plan for this launch
+ * shape, 0 for an unsupported shape. Arguments as cie_paged_workspace_bytes.
+ *
+ * cie_paged_plan: fills `plan` (host memory, at least cie_paged_plan_bytes)
+ * from host arrays context_lens [B] and block_tables [B rows of
+ * block_table_row_stride ints]. for_append: 1 when the plan is for a launch
+ * with k_new / v_new (cie_paged_fwd_ex), whose contexts must count their Lq
+ * new tokens. Returns the number of sequences split across workgroups
+ * (>= 0; pass it to cie_paged_fwd_ex as plan_split: with 0 the merge pass
+ * is not launched and no workspace is needed), or a negative CIE_E* code.
+ * Context lengths and block ids are validated here as cie_paged_fwd
+ * validates them (NaN output, never an out-of-range read).
+ */
+size_t cie_paged_plan_bytes(int B, int Hq, int Hk, int Lq, int D, int max_context, int block_size,
+                            int max_blocks_per_seq);
+int cie_paged_plan(void* plan, size_t plan_bytes, const int32_t* context_lens, const int32_t* block_tables,
+                   int64_t block_table_row_stride, int B, int Hq, int Hk, int Lq, int D, int num_blocks,
+                   int block_size, int max_blocks_per_seq, int max_context, int for_append);
+
+/*
+ * One entry for every paged attention variant: cie_paged_fwd with, each
+ * optional, the fused append (k_new, v_new non-NULL: cie_paged_fwd_append),
+ * RoPE (rope_cos, rope_sin non-NULL: the _rope entries) and a device copy of
+ * a plan from cie_paged_plan (plan non-NULL; plan_split = its return value;
+ * block_tables and context_lens are then not read and may be NULL). The
+ * results equal the corresponding entry's bit for bit. The workspace must
+ * hold cie_paged_workspace_bytes bytes; with a plan whose plan_split is 0 it
+ * may be NULL. A plan built for other arguments than this call's (checked
+ * through its header on the device) gives NaN outputs.
+ */
+int cie_paged_fwd_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                     const int32_t* block_tables, const int32_t* context_lens, const void* plan, int plan_split,
+                     void* o, void* workspace, size_t workspace_bytes,
+                     const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
+                     const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,
+                     int B, int Hq, int Hk, int Lq, int D,
+                     int num_blocks, int block_size, int max_blocks_per_seq,
+                     int max_context, float scale, int causal, int dtype,
+                     const void* rope_cos, const void* rope_sin, int rope_rows, int rope_dtype,
+                     void* stream);
+
+/*
  * cie_paged_fwd without a caller workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture that must not call the
  * allocator, tight serving loops, harnesses that forbid hipMalloc). No

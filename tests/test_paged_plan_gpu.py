@@ -1,0 +1,147 @@
+"""GPU parity of planned paged attention (a host-built work plan,
+cie_paged_plan + cie_paged_fwd_ex) against the unplanned launch that derives
+the same schedule on the device (cie_paged_fwd and its append / RoPE
+variants): the same ranges, pieces and arithmetic, so outputs and pools must
+be equal bit for bit; and against the oracle (the reference's gather then
+dense attention, engine/model/block.py:56-71) within tolerance."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+from engine import _lib
+from engine.attention import paged_attention, paged_plan
+from oracle import paged_attention_ref
+from test_flash_gpu import TOL, assert_close
+from test_paged_gpu import make_paged
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _both(q, kp, vp, bt, lt, **kw):
+    B, Hq, Lq, D = q.shape
+    nb, bs, Hk, _ = kp.shape
+    args = [t.to(DEV) for t in (q, kp, vp, bt, lt)]
+    plain = paged_attention(*args, causal=True, **kw)
+    pl = paged_plan(lt, bt, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb, block_size=bs,
+                    max_context=kw.get("max_context"), device=DEV)
+    planned = paged_attention(*args, causal=True, plan=pl, **kw)
+    return plain.cpu(), planned.cpu(), pl
+
+
+@pytest.mark.parametrize("name", ["decode_b32", "verify_b8"])
+def test_workloads_planned_equal_unplanned(name):
+    from benchmarks import workloads
+
+    c = workloads.WORKLOADS[name]()
+    plain, planned, pl = _both(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens,
+                               max_context=int(c.context_lens.max()))
+    assert pl.split > 0
+    assert torch.equal(planned, plain)
+    ref = paged_attention_ref(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens, causal=True)
+    assert_close(planned, ref, TOL[c.q.dtype], name)
+
+
+@pytest.mark.parametrize("Lq,bs,D,dtype", [(1, 16, 64, torch.float16), (5, 3, 128, torch.bfloat16),
+                                           (3, 16, 16, torch.float16), (2, 7, 256, torch.bfloat16),
+                                           (1, 1, 32, torch.float16)])
+def test_ragged_and_invalid_planned_equal_unplanned(Lq, bs, D, dtype):
+    # empty history, lengths below / around tile and block boundaries, an invalid
+    # length (longer than the table allows) and an invalid block id
+    lens = [0, Lq, 31 + Lq, 33, 700, 2049, 95, 1024 + Lq, 5000]
+    q, kp, vp, bt, lt = make_paged(lens[:-1] + [64], Lq, D, dtype, bs, Hq=8, Hk=2, seed=D + bs, vscale=0.5)
+    lt[-1] = 5000  # beyond max_blocks * block_size of its row
+    bt[4, 2] = kp.shape[0] + 7
+    plain, planned, _ = _both(q, kp, vp, bt, lt)
+    assert torch.equal(torch.isnan(planned), torch.isnan(plain))
+    assert torch.equal(planned.nan_to_num(7.0), plain.nan_to_num(7.0))
+    assert torch.isnan(planned[4]).all() and torch.isnan(planned[8]).all()
+    assert (planned[0] == 0).all()
+
+
+def test_plan_without_split_skips_the_merge():
+    lens = [32] * 48 + [7]  # one tile per sequence
+    q, kp, vp, bt, lt = make_paged(lens, 1, 64, torch.float16, 16, Hq=32, Hk=8, seed=3)
+    plain, planned, pl = _both(q, kp, vp, bt, lt)
+    assert pl.split == 0
+    assert torch.equal(planned, plain)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("Lq,dtype", [(1, torch.float16), (5, torch.bfloat16)])
+def test_planned_fused_append_equals_unplanned(Lq, dtype, rope):
+    from engine.model.rope import RotaryEmbedding
+
+    lens = [Lq, 40 + Lq, 700, 2049, 4096, 33]
+    q, kp, vp, bt, lt = make_paged(lens, Lq, 64, dtype, 16, Hq=8, Hk=2, seed=Lq, vscale=0.5)
+    g = torch.Generator().manual_seed(9)
+    kn = torch.randn(len(lens) * Lq, 2, 64, generator=g).to(dtype)
+    vn = (torch.randn(len(lens) * Lq, 2, 64, generator=g) * 0.5).to(dtype)
+    kw = {"rope": RotaryEmbedding(64, 8192).to(DEV).tables} if rope else {}
+    outs, pools = [], []
+    for planned in (False, True):
+        kd, vd = kp.to(DEV), vp.to(DEV)
+        pl = paged_plan(lt, bt, Hq=8, Hk=2, Lq=Lq, D=64, num_blocks=kp.shape[0], block_size=16,
+                        for_append=True, device=DEV) if planned else None
+        o = paged_attention(q.to(DEV), kd, vd, bt.to(DEV), lt.to(DEV), causal=True,
+                            new_kv=(kn.to(DEV), vn.to(DEV)), plan=pl, **kw)
+        outs.append(o.cpu())
+        pools.append((kd.cpu(), vd.cpu()))
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(pools[0][0], pools[1][0]) and torch.equal(pools[0][1], pools[1][1])
+
+
+def test_plan_for_other_arguments_is_rejected_or_gives_nan():
+    q, kp, vp, bt, lt = make_paged([40, 300], 1, 64, torch.float16, 16, seed=5)
+    args = [t.to(DEV) for t in (q, kp, vp, bt, lt)]
+    pl = paged_plan(lt, bt, Hq=8, Hk=2, Lq=1, D=64, num_blocks=kp.shape[0], block_size=16, for_append=True,
+                    device=DEV)
+    with pytest.raises(ValueError):  # the Python layer checks the key
+        paged_attention(*args, plan=pl)
+    # through the C ABI the device checks the plan's header: a plan built for the fused
+    # append used by a plain launch gives NaN rows rather than reading past anything
+    lib = _lib.load()
+    o = torch.zeros_like(args[0])
+    st = [_lib.strides(t) for t in (args[0], args[1], args[2], o)]
+    none3 = (ctypes.c_int64 * 3)(0, 0, 1)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    rc = lib.cie_paged_fwd_ex(args[0].data_ptr(), None, None, args[1].data_ptr(), args[2].data_ptr(), None, None,
+                              pl.data.data_ptr(), pl.split, o.data_ptr(), ws.data_ptr(), ws.numel(),
+                              st[0], none3, none3, st[1], st[2], st[3], 2, 8, 2, 1, 64, kp.shape[0], 16, bt.shape[1],
+                              0, ctypes.c_float(0.125), 1, 0, None, None, 0, 0,
+                              _lib.stream_handle(torch.device(DEV)))
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    assert torch.isnan(o).all()
+
+
+def test_attention_section_with_step_plan_equals_without():
+    """A decode step and a verify step through attention_section, with the
+    plan built by prepare_step(num_heads=...) and without it."""
+    from engine.cache import KVCacheConfig, PagedKVCache
+    from engine.model import attention_section
+
+    for L, dtype in ((1, torch.float16), (4, torch.bfloat16)):
+        B, Hq, Hk, D = 5, 8, 2, 64
+        outs = []
+        for use_plan in (False, True):
+            cache = PagedKVCache(KVCacheConfig(1, Hk, D, 400, 16, dtype, DEV))
+            g = torch.Generator().manual_seed(L)
+            tables = [cache.new_sequence() for _ in range(B)]
+            for t, n in zip(tables, [50, 0, 300, 1000, 17]):
+                if n:
+                    cache.append(0, t, torch.randn(n, Hk, D, generator=g).to(dtype).to(DEV),
+                                 torch.randn(n, Hk, D, generator=g).to(dtype).to(DEV))
+            q = torch.randn(B, Hq, L, D, generator=g).to(dtype).to(DEV)
+            k = torch.randn(B, Hk, L, D, generator=g).to(dtype).to(DEV)
+            v = torch.randn(B, Hk, L, D, generator=g).to(dtype).to(DEV)
+            step = cache.prepare_step(tables, L, num_heads=Hq if use_plan else None)
+            assert (step.plan is not None) == use_plan
+            outs.append((attention_section(q, k, v, 0, cache, step).cpu(), cache.k[0].cpu(), cache.v[0].cpu()))
+        for a, b in zip(outs[0], outs[1]):
+            assert torch.equal(a, b)
