@@ -26,7 +26,7 @@ reference's slice copies, since no kernel runs there.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Sequence
 
 import torch
@@ -56,8 +56,10 @@ class StepBatch:
     (:meth:`PagedKVCache.prepare_step`), read by every layer's append and
     paged attention: int32 block tables (B, max_blocks), context lengths (B,)
     including the step's new tokens, row offsets ``cu_new`` (B+1,) of the
-    new tokens (``num_new`` per sequence) and their start positions (B,).
-    ``max_context`` bounds ``context_lens``."""
+    new tokens and their start positions (B,). ``num_new`` is the number of
+    new tokens of every sequence, or -1 when the counts differ (a ragged
+    step: a prefill chunk next to decode tokens); ``new_counts`` holds them
+    per sequence. ``max_context`` bounds ``context_lens``."""
     block_tables: torch.Tensor
     context_lens: torch.Tensor
     cu_new: torch.Tensor
@@ -68,6 +70,16 @@ class StepBatch:
     starts_host: tuple = ()      # host copies of starts and context lengths
     lengths_host: tuple = ()
     plan: object = None          # engine.attention.PagedPlan of the step's paged launches, or None
+    new_counts: tuple = ()       # new tokens per sequence (host)
+    cache: dict = field(default_factory=dict, repr=False)  # device index tensors of ragged steps, built once
+
+    @property
+    def total_new(self) -> int:
+        return sum(self.new_counts)
+
+    @property
+    def max_new(self) -> int:
+        return max(self.new_counts + (0,))
 
     def plan_for(self, append: bool):
         """The step's paged-attention plan if it was built for a launch with
@@ -80,14 +92,14 @@ class StepBatch:
     def fresh(self) -> bool:
         """Every sequence holds exactly this step's tokens (a prefill from
         position 0): attention needs only the new K/V, no history."""
-        return all(s0 == 0 and n == self.num_new for s0, n in zip(self.starts_host, self.lengths_host))
+        return all(s0 == 0 and n == c for s0, n, c in zip(self.starts_host, self.lengths_host, self.new_counts))
 
     @property
     def aligned(self) -> bool:
-        """The new tokens are the newest of every sequence (start + num_new
-        == context length), so their positions are context_len - num_new + i,
-        as the paged kernel's fused RoPE assumes."""
-        return all(s0 + self.num_new == n for s0, n in zip(self.starts_host, self.lengths_host))
+        """The new tokens are the newest of every sequence (start + count ==
+        context length), so their positions are context_len - count + i, as
+        the paged kernel's fused RoPE assumes."""
+        return all(s0 + c == n for s0, n, c in zip(self.starts_host, self.lengths_host, self.new_counts))
 
 
 def block_table_tensor(
@@ -269,15 +281,16 @@ class PagedKVCache:
                 done += n
         table.length = max(table.length, end)
 
-    def prepare_step(self, tables: Sequence[BlockTable], num_new: int, starts: Sequence[int] | None = None,
-                     max_blocks: int | None = None, *, num_heads: int | None = None,
-                     fused_append: bool | None = None) -> "StepBatch":
+    def prepare_step(self, tables: Sequence[BlockTable], num_new: int | Sequence[int],
+                     starts: Sequence[int] | None = None, max_blocks: int | None = None, *,
+                     num_heads: int | None = None, fused_append: bool | None = None) -> "StepBatch":
         """Host side of one engine step for a batch: allocate the blocks the
-        ``num_new`` tokens of every sequence need (at ``starts[b]``, default
-        each table's end), extend the lengths, and upload everything the
-        step's kernels read (block tables, context lengths, the row offsets
-        and start positions of the new tokens) in ONE host-to-device copy.
-        Every layer's :meth:`append_step` and ``paged_attention`` of the step
+        ``num_new`` tokens of every sequence need (one count for all, or one
+        per sequence for a ragged step; at ``starts[b]``, default each
+        table's end), extend the lengths, and upload everything the step's
+        kernels read (block tables, context lengths, the row offsets and
+        start positions of the new tokens) in ONE host-to-device copy. Every
+        layer's :meth:`append_step` and ``paged_attention`` of the step
         reuses it, so no layer touches the host.
 
         ``num_heads`` (the model's query heads): also build the work plan of
@@ -289,12 +302,16 @@ class PagedKVCache:
         if self.device.type != "cuda":
             raise RuntimeError("prepare_step requires a CUDA cache")
         starts = [t.length for t in tables] if starts is None else list(starts)
-        if len(starts) != len(tables) or num_new < 0 or any(s < 0 for s in starts):
-            raise ValueError(f"bad step: {len(tables)} tables, starts {starts}, num_new {num_new}")
-        for t, s0 in zip(tables, starts):
-            while len(t.blocks) < t.num_blocks_needed(s0 + num_new):
+        counts = [int(num_new)] * len(tables) if isinstance(num_new, int) else [int(c) for c in num_new]
+        if len(starts) != len(tables) or len(counts) != len(tables) or any(c < 0 for c in counts) \
+                or any(s < 0 for s in starts):
+            raise ValueError(f"bad step: {len(tables)} tables, starts {starts}, new tokens {num_new}")
+        uniform = len(set(counts)) <= 1
+        num_new = counts[0] if counts and uniform else (0 if not counts else -1)
+        for t, s0, c in zip(tables, starts, counts):
+            while len(t.blocks) < t.num_blocks_needed(s0 + c):
                 t.blocks.append(self._alloc_block())
-            t.length = max(t.length, s0 + num_new)
+            t.length = max(t.length, s0 + c)
         B = len(tables)
         width = max([len(t.blocks) for t in tables] + [1]) if max_blocks is None else max_blocks
         lengths = tuple(t.length for t in tables)
@@ -302,7 +319,7 @@ class PagedKVCache:
         o = B * width
         meta = o + 3 * B + 1
         n_plan = 0
-        if num_heads is not None:
+        if num_heads is not None and num_new > 0:  # a plan covers one launch shape: uniform steps only
             from engine.attention import paged_plan_ints
 
             n_plan = paged_plan_ints(B, num_heads, self.cfg.num_kv_heads, num_new, self.cfg.head_dim,
@@ -315,13 +332,16 @@ class PagedKVCache:
             if t.blocks:
                 host[i * width:i * width + len(t.blocks)] = torch.tensor(t.blocks, dtype=torch.int32)
         host[o:o + B] = torch.tensor(lengths, dtype=torch.int32)
-        host[o + B:o + 2 * B + 1] = torch.arange(B + 1, dtype=torch.int32) * num_new
+        cu = [0]
+        for c in counts:
+            cu.append(cu[-1] + c)
+        host[o + B:o + 2 * B + 1] = torch.tensor(cu, dtype=torch.int32)
         host[o + 2 * B + 1:meta] = torch.tensor(starts, dtype=torch.int32)
         split = key = None
         if n_plan:
             from engine.attention import paged_plan_fill
 
-            append = all(s0 + num_new == n for s0, n in zip(starts, lengths)) if fused_append is None \
+            append = all(s0 + c == n for s0, n, c in zip(starts, lengths, counts)) if fused_append is None \
                 else fused_append
             split, key = paged_plan_fill(host[p0:p0 + n_plan], host[o:o + B], host[:o].view(B, width),
                                          Hq=num_heads, Hk=self.cfg.num_kv_heads, Lq=num_new, D=self.cfg.head_dim,
@@ -336,23 +356,22 @@ class PagedKVCache:
         return StepBatch(block_tables=dev[:o].view(B, width), context_lens=dev[o:o + B],
                          cu_new=dev[o + B:o + 2 * B + 1], starts=dev[o + 2 * B + 1:meta], num_new=num_new,
                          max_context=max_context, tables=tuple(tables), starts_host=tuple(starts),
-                         lengths_host=lengths, plan=plan)
+                         lengths_host=lengths, plan=plan, new_counts=tuple(counts))
 
     def append_step(self, layer: int, step: "StepBatch", k: torch.Tensor, v: torch.Tensor, *,
                     rope: tuple[torch.Tensor, torch.Tensor] | None = None,
                     k_out: torch.Tensor | None = None) -> None:
         """Write one layer's new K/V rows of a prepared step: k, v are
-        (B * num_new, Hk, D), the rows of sequence b consecutive. One
+        (total new tokens, Hk, D), the rows of sequence b consecutive. One
         ``cie_kv_append`` launch; no host work, no host-to-device copy, so a
         step's layers can be captured in one HIP graph. ``rope`` / ``k_out``
         as in :func:`kv_append` (K rotated at its position on the way in)."""
         self._validate(k)
         self._validate(v)
-        B = step.context_lens.shape[0]
-        if k.shape[0] != B * step.num_new or v.shape[0] != k.shape[0]:
-            raise ValueError(f"append_step expects {B * step.num_new} rows, got {k.shape[0]}, {v.shape[0]}")
+        if k.shape[0] != step.total_new or v.shape[0] != k.shape[0]:
+            raise ValueError(f"append_step expects {step.total_new} rows, got {k.shape[0]}, {v.shape[0]}")
         kv_append(k, v, self.k[layer], self.v[layer], step.block_tables, step.cu_new, step.starts,
-                  max_new=step.num_new, rope=rope, k_out=k_out)
+                  max_new=step.max_new, rope=rope, k_out=k_out)
 
     def append_batch(self, layer: int, tables: Sequence[BlockTable], k: torch.Tensor, v: torch.Tensor,
                      lengths: Sequence[int], starts: Sequence[int] | None = None,

@@ -40,7 +40,9 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions:
                out: torch.Tensor | None = None, status: torch.Tensor | None = None) -> torch.Tensor:
     """RoPE of x (B, H, L, D) on the GPU, as ``apply_rotary_ref``
     (kernels/ref/rope_apply_ref.py:22-53): positions (L,), (B, L) or None
-    (0..L-1); cos / sin the fp32 (rows, D/2) tables on x's device. Returns
+    (0..L-1); cos / sin the (rows, D/2) tables on x's device, fp32 or cast
+    to fp16 / bf16 (then rotated with 16-bit arithmetic, as torch does when
+    the reference engine casts the model's buffers). Returns
     ``out`` (a new tensor by default; ``out=x`` rotates in place). A position
     outside the tables gives a NaN row and ORs 2 into ``status`` (optional
     int32 (1,) on the device) where the reference's indexing raises."""
