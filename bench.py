@@ -100,7 +100,7 @@ def traffic_probe(names=("prefill_s2048", "decode_b32", "verify_b8")):
     del x, y
     for name in names:
         case = workloads.WORKLOADS[name]()
-        launch = FlashLaunch(case, dev) if name.startswith("prefill") else PagedLaunch(case, dev)
+        launch = FlashLaunch(case, dev) if name.startswith("prefill") else PagedLaunch(case, dev, planned=True)
         for i in range(3):
             launch(i)
         torch.cuda.synchronize()
@@ -124,11 +124,12 @@ class FlashLaunch:
         self._keep = [_lib.strides(t) for t in (self.q, self.k, self.v, self.o)]
         self.args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(),
                      *self._keep, B, H, Hk, M, N, D, ctypes.c_float(1.0 / math.sqrt(D)), 1,
-                     _lib.DTYPE_CODES[self.q.dtype], _lib.stream_handle(self.q.device))
+                     _lib.DTYPE_CODES[self.q.dtype])
+        self.dev = self.q.device
         self.flops = case.flops
 
     def __call__(self, i=0):
-        rc = self.lib.cie_flash_fwd(*self.args)
+        rc = self.lib.cie_flash_fwd(*self.args, _stream(self.dev))
         if rc:
             from engine import _lib
             _lib.check(rc)
@@ -489,9 +490,10 @@ def settle(fn, seconds=SETTLE_S):
         torch.cuda.synchronize()
 
 
-def event_time_ms(fn, n, warmup, trials=3):
+def event_time_ms(fn, n, warmup, trials=3, mark=None):
     """Median over trials of (HIP-event time of n back-to-back launches) / n,
-    after `warmup` launches and a settle phase."""
+    after `warmup` launches and a settle phase. `mark` (optional): called at
+    the start of each trial, its results collected in `event_time_ms.marks`."""
     import torch
 
     for i in range(warmup):
@@ -499,7 +501,10 @@ def event_time_ms(fn, n, warmup, trials=3):
     settle(fn)
     torch.cuda.synchronize()
     res = []
+    event_time_ms.marks = []
     for _ in range(trials):
+        if mark is not None:
+            event_time_ms.marks.append(mark())
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record()
@@ -511,15 +516,21 @@ def event_time_ms(fn, n, warmup, trials=3):
     return statistics.median(res)
 
 
-def _timed(fn, runs):
-    """fn() once untimed, then the median wall time of `runs` calls."""
+def _timed(fn, runs, min_run_s=0.25):
+    """fn() once untimed, then the median over `runs` timed runs of the wall
+    time per call, each run repeating fn enough times to last about
+    `min_run_s` (a single call of a small case is too short for the clock).
+    Returns (seconds per call, calls per run)."""
+    t0 = time.perf_counter()
     fn()
+    reps = max(1, math.ceil(min_run_s / max(time.perf_counter() - t0, 1e-6)))
     times = []
     for _ in range(runs):
         t0 = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t0)
-    return statistics.median(times)
+        for _ in range(reps):
+            fn()
+        times.append((time.perf_counter() - t0) / reps)
+    return statistics.median(times), reps
 
 
 def cpu_baselines(names=("prefill_s128", "prefill_s2048", "decode_b32", "verify_b8", "prefill_s16384")):
@@ -547,14 +558,15 @@ def cpu_baselines(names=("prefill_s128", "prefill_s2048", "decode_b32", "verify_
                 # bounded sample: batch 0, kv head 0 with its 4 query heads (1/8 of the work), every
                 # query row, chunked over 2048-row query blocks (the full score matrix is 34 GB)
                 qs, ks, vs = q[:, :4], k[:, :1], v[:, :1]
-                t = _timed(lambda: flash_attention_ref_chunked(qs, ks, vs, causal=True, q_chunk=2048), 1)
+                t, _ = _timed(lambda: flash_attention_ref_chunked(qs, ks, vs, causal=True, q_chunk=2048), 1)
                 flops = c.flops / 8
                 sample = (f"kv head 0 with its 4 query heads over all 16384 rows (1/8 of the workload), "
                           f"fp32 oracle chunked over 2048-row query blocks, 1 run, {t:.2f} s")
             else:
-                t = _timed(lambda: flash_attention_ref(q, k, v, causal=True), 3)
+                t, reps = _timed(lambda: flash_attention_ref(q, k, v, causal=True), 3)
                 flops = c.flops
-                sample = f"full {name} workload through the unchunked fp32 oracle, median of 3 runs, {t:.3f} s each"
+                sample = (f"full {name} workload through the unchunked fp32 oracle, median of 3 runs of {reps} "
+                          f"call(s), {t * 1e3:.2f} ms per call")
             out[name] = {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
                          "kind": "port", "sample": sample}
         else:
@@ -567,11 +579,12 @@ def cpu_baselines(names=("prefill_s128", "prefill_s2048", "decode_b32", "verify_
                     vd = gather_ref(c.v_pool, c.block_tables[b], lens[b]).float().transpose(0, 1).unsqueeze(0)
                     flash_attention_ref(c.q[b:b + 1].float(), kd, vd, causal=True)
 
-            t = _timed(per_sequence, 3)
+            t, reps = _timed(per_sequence, 3)
             out[name] = {"value": round(c.bytes / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
                          "kind": "port",
                          "sample": f"full {name} workload, per sequence: gather through the block table, then "
-                                   f"the fp32 oracle with Lq={Lq}; median of 3 runs, {t:.3f} s each"}
+                                   f"the fp32 oracle with Lq={Lq}; median of 3 runs of {reps} call(s), "
+                                   f"{t * 1e3:.2f} ms per call"}
     return out
 
 
@@ -596,14 +609,23 @@ def main():
     case = workloads.prefill_s2048()
     q, k, v = case.q.to(dev), case.k.to(dev), case.v.to(dev)
 
-    # headline: K steps of the public entry point (after an untimed clock settle and W warmup steps)
-    settle(lambda i=0: flash_attention(q, k, v, causal=True))
-    for _ in range(args.warmup):
+    # Launches of the prefill kernel (2048 workgroups) are counted in launch
+    # order, so a kernel trace of this run can pick out the timed ones.
+    launches = [0]
+
+    def headline(i=0):
         flash_attention(q, k, v, causal=True)
+        launches[0] += 1
+
+    # headline: K steps of the public entry point (after an untimed clock settle and W warmup steps)
+    settle(headline)
+    for _ in range(args.warmup):
+        headline()
     torch.cuda.synchronize()
+    first_timed = launches[0]
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        flash_attention(q, k, v, causal=True)
+        headline()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
@@ -611,7 +633,17 @@ def main():
 
     # roofline of the prefill kernel: event-timed back-to-back launches
     fl = FlashLaunch(case, dev)
-    kern_ms = event_time_ms(fl, max(20, args.steps), 3)
+
+    def roof(i=0):
+        fl(i)
+        launches[0] += 1
+
+    n_roof = max(20, args.steps)
+    kern_ms = event_time_ms(roof, n_roof, 3, mark=lambda: launches[0])
+    print("[bench-launches] " + json.dumps({
+        "kernel": "flash_fwd_kernel<0, 64>", "workgroups": 2048, "workload": "prefill_s2048",
+        "headline_steps": [first_timed, args.steps],
+        "roofline_trials": [[m, n_roof] for m in event_time_ms.marks]}), file=sys.stderr, flush=True)
     achieved = case.flops / (kern_ms / 1e3) / 1e12
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": traffic_from_summary(),
