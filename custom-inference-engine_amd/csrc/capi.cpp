@@ -284,6 +284,8 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   CIE_TRY(check_strides("o", o_stride));
   CIE_TRY(check_strides("k_cache", kc_stride));
   CIE_TRY(check_strides("v_cache", vc_stride));
+  if ((int64_t)(Hk > 0 ? Hk - 1 : 0) * std::max(kc_stride[2], vc_stride[2]) + D >= ((int64_t)1 << 31))
+    return fail(CIE_EINVAL, "k_cache / v_cache: the kv heads of a token span 2^31 elements or more");
   if (k_new || v_new) {
     CIE_TRY(check_ptr("k_new", k_new));
     CIE_TRY(check_ptr("v_new", v_new));

@@ -318,9 +318,13 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   // the tile, i.e. token P / NCH, stored chunk P % NCH, which holds chunk
   // (P % NCH) ^ row_swizzle(token) of the token's group row.
   int ltok[C::DPW];
-  int64_t goffk[C::DPW], goffv[C::DPW];
+  int32_t goffk[C::DPW], goffv[C::DPW];  // head + column offsets (the host bounds them below 2^31)
+  // Fused append: the chunk's (head, column) within a new-token row, kept as
+  // the chunk index only; the offsets are formed on the few tiles that hold
+  // new tokens (keeping them as 64-bit offsets pushed the kernel past the
+  // register file, and the spill reloads waited for every copy in flight).
   constexpr int NA = APPEND ? C::DPW : 1;
-  int64_t gnk[NA], gnv[NA];  // the same chunk in a new-token row (fused append)
+  int nch_of[NA];
 #pragma unroll
   for (int x = 0; x < C::DPW; ++x) {
     const int P = 64 * (hh * C::DPW + x) + lane;
@@ -328,12 +332,9 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     const int c = (P & (NCH - 1)) ^ row_swizzle(NCH, tk);
     const int hd = c / C::S, dc = c % C::S;
     ltok[x] = tk;
-    goffk[x] = (int64_t)(gh * p.Hg + hd) * p.ks2 + 8 * dc;
-    if constexpr (APPEND) {
-      gnk[x] = (int64_t)(gh * p.Hg + hd) * p.kns1 + 8 * dc;
-      gnv[x] = (int64_t)(gh * p.Hg + hd) * p.vns1 + 8 * dc;
-    }
-    goffv[x] = (int64_t)(gh * p.Hg + hd) * p.vs2 + 8 * dc;
+    goffk[x] = (gh * p.Hg + hd) * (int32_t)p.ks2 + 8 * dc;
+    if constexpr (APPEND) nch_of[x] = c;
+    goffv[x] = (gh * p.Hg + hd) * (int32_t)p.vs2 + 8 * dc;
   }
   // Fragment reads: K row l32 (chunk 2 kk + hl of head hh), V^T rows.
   const int swk = row_swizzle(NCH, l32);
@@ -385,8 +386,11 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         const uint16_t *sk, *sv;
         if (tk >= i_ctx - p.Lq) {
           const int64_t row = (int64_t)i_b * p.Lq + (tk - (i_ctx - p.Lq));
-          sk = p.kn + row * p.kns0 + gnk[APPEND ? x : 0];
-          sv = p.vn + row * p.vns0 + gnv[APPEND ? x : 0];
+          int c = nch_of[APPEND ? x : 0];
+          asm volatile("" : "+v"(c));  // keeps the offset arithmetic on this path (not hoisted and kept live)
+          const int hd = gh * p.Hg + c / C::S, col = 8 * (c % C::S);
+          sk = p.kn + row * p.kns0 + (int64_t)hd * p.kns1 + col;
+          sv = p.vn + row * p.vns0 + (int64_t)hd * p.vns1 + col;
         } else {
           const int blk = (int)fdiv((uint32_t)tk, p.bsdiv);
           const int off = tk - blk * p.block_size;
@@ -423,10 +427,12 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
     if (p.narrow) {
 #pragma unroll
       for (int x = 0; x < C::DPW; ++x) {
-        const uint32_t base_k = __umul24(bid[x], p.ks0_24) + __umul24(off[x], p.ks1_24);
-        const uint32_t base_v = __umul24(bid[x], p.vs0_24) + __umul24(off[x], p.vs1_24);
-        dma16_at_nt(p.kc + base_k + goffk[x], st + 1024u * x);
-        dma16_at_nt(p.vc + base_v + goffv[x], st + 2u * TILE_EL + 1024u * x);
+        // whole 32-bit element offsets (the narrow path bounds them below 2^31),
+        // added to the pool base once: no per-lane 64-bit pointers stay live
+        const uint32_t ek = __umul24(bid[x], p.ks0_24) + __umul24(off[x], p.ks1_24) + (uint32_t)goffk[x];
+        const uint32_t ev = __umul24(bid[x], p.vs0_24) + __umul24(off[x], p.vs1_24) + (uint32_t)goffv[x];
+        dma16_at_nt(p.kc + ek, st + 1024u * x);
+        dma16_at_nt(p.vc + ev, st + 2u * TILE_EL + 1024u * x);
       }
     } else {
 #pragma unroll
