@@ -108,6 +108,9 @@ def _paged(**over):
     (dict(ws=0), _lib.CIE_EWORKSPACE),
     (dict(ws_bytes=16), _lib.CIE_EWORKSPACE),
     (dict(mb=1 << 28, bs=16), _lib.CIE_EINVAL),
+    # the kv heads of one token spanning 2^31 elements (per-lane head offsets are 32-bit)
+    (dict(ks=_st(8 << 32, 8 << 29, 1 << 29, 1)), _lib.CIE_EINVAL),
+    (dict(vs=_st(8 << 32, 8 << 29, 1 << 29, 1)), _lib.CIE_EINVAL),
 ])
 def test_paged_rejects_bad_arguments(over, code):
     assert _paged(**over) == code
