@@ -354,15 +354,6 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   int i_ctx = __builtin_amdgcn_readfirstlane(ent[0][1]), i_ttlo = __builtin_amdgcn_readfirstlane(ent[0][2]);
   int i_idb = __builtin_amdgcn_readfirstlane(ent[0][4]), i_blk = __builtin_amdgcn_readfirstlane(ent[0][5]);
   int i_stage = 0;
-  // With 1 KiB token rows (NCH == 64) every copy instruction moves one token
-  // row: a scalar token base plus a per-lane chunk offset fixed across tiles.
-  const bool row_copies = NCH == 64 && (int64_t)(p.Hk - 1) * max(p.ks2, p.vs2) + D < ((int64_t)1 << 30);
-  uint32_t voffk[C::DPW], voffv[C::DPW];
-#pragma unroll
-  for (int x = 0; x < C::DPW; ++x) {
-    voffk[x] = row_copies ? (uint32_t)(2 * goffk[x]) : 0u;
-    voffv[x] = row_copies ? (uint32_t)(2 * goffv[x]) : 0u;
-  }
   auto issue = [&](int k) {
     if (k == i_end) {
       ++ie;
@@ -400,19 +391,6 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         }
         dma16_at_nt(sk, st + 1024u * x);
         dma16_at_nt(sv, st + 2u * TILE_EL + 1024u * x);
-      }
-      return;
-    }
-    if (row_copies) {
-#pragma unroll
-      for (int x = 0; x < C::DPW; ++x) {
-        const int tk = min(tbase + hh * C::DPW + x, i_ctx - 1);
-        const int blk = (int)fdiv((uint32_t)tk, p.bsdiv);
-        const int off = tk - blk * p.block_size;
-        const int bid = __builtin_amdgcn_readfirstlane(max(sbt[i_idb + blk - i_blk], 0));
-        dma16_sv_nt(uniform_ptr(p.kc + (int64_t)bid * p.ks0 + (int64_t)off * p.ks1), voffk[x], st + 1024u * x);
-        dma16_sv_nt(uniform_ptr(p.vc + (int64_t)bid * p.vs0 + (int64_t)off * p.vs1), voffv[x],
-                 st + 2u * TILE_EL + 1024u * x);
       }
       return;
     }
