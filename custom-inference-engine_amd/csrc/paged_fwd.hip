@@ -43,6 +43,7 @@
 #include <climits>
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 #include "kernels.hpp"
 #include "rope.hpp"
@@ -50,6 +51,9 @@
 namespace cie {
 
 constexpr float kLazyRescalePaged = 8.0f;
+
+// Lambdas of the kernel are inlined: the arrays they touch stay in registers.
+#define CIE_PAGED_INLINE __attribute__((always_inline))
 
 template <int D>
 struct PagedCfg {
@@ -457,14 +461,11 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
   float m = -INFINITY, l = 0.f;
   const float c = p.scale_log2;
 
-  for (int n = 0; n < T; ++n) {
-    if (issuer) {
-      if (n + NST - 1 < T) issue(n + NST - 1);
-      wait_tiles_ahead<C::DPW>(min(NST - 1, T - 1 - n));
-    }
-    __syncthreads();  // tile n is in LDS for every wave
-
-    if (n == c_end) {  // first tile of the next sequence piece
+  // First tile of the next sequence piece. FIRST: the piece of the range's
+  // first tile, set up before the tile loop, so the q rows preloaded for it
+  // are dead inside the loop when no later piece uses them (QPRE = 1).
+  auto begin_piece = [&](const int n, auto FIRST) CIE_PAGED_INLINE {
+    {
       ++ce;
       c_base = n;
       c_end = n + ent[ce][3];
@@ -478,9 +479,12 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
         for (int x = lane; x < blk_hi - blk_lo + 1; x += 64) bad |= sbt[idb + x] < 0;
         poison = __builtin_amdgcn_ballot_w64(bad) != 0;
       }
-      if (ce < C::QPRE) {
+      if (decltype(FIRST)::value && C::QPRE > 0) {
 #pragma unroll
-        for (int e = 0; e < C::QPRE; ++e)
+        for (int kk = 0; kk < C::KK; ++kk) qf[kk] = qpre[0][kk];
+      } else if (!decltype(FIRST)::value && C::QPRE > 1 && ce < C::QPRE) {
+#pragma unroll
+        for (int e = 1; e < C::QPRE; ++e)
           if (e == ce)
 #pragma unroll
             for (int kk = 0; kk < C::KK; ++kk) qf[kk] = qpre[e][kk];
@@ -500,6 +504,17 @@ __global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const Pa
       lim = p.causal ? c_ctx - p.Lq + i : c_ctx - 1;
       lim_min = p.causal ? c_ctx - p.Lq : c_ctx - 1;
     }
+  };
+  begin_piece(0, std::true_type{});
+
+  for (int n = 0; n < T; ++n) {
+    if (issuer) {
+      if (n + NST - 1 < T) issue(n + NST - 1);
+      wait_tiles_ahead<C::DPW>(min(NST - 1, T - 1 - n));
+    }
+    __syncthreads();  // tile n is in LDS for every wave
+
+    if (n > 0 && n == c_end) begin_piece(n, std::false_type{});
 
     const uint16_t* kst = ring + c_stage * STAGE_EL;
     const uint16_t* vst = kst + TILE_EL;
