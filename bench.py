@@ -651,7 +651,8 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        for name in ("decode_b32", "verify_b8"):
+        # the paged workloads, and the same shapes at head_dim 128
+        for name in ("decode_b32", "verify_b8", "decode_b32_d128", "verify_b8_d128"):
             c = workloads.WORKLOADS[name]()
             # with the host-built plan (what an engine step uses, uploaded once for all layers) and
             # with the schedule derived on the device from the lengths alone

@@ -11,6 +11,7 @@ scale 1/sqrt(D), 32 query heads over 8 kv heads.
   decode_b32       B=32 Lq=1 ctx~U{256..4096}  bs=16 fp16 N(0,1)   seed 2
   verify_b8        B=8  Lq=5 ctx~U{1024..8192} bs=16 bf16 N(0,1)   seed 3
   prefill_s16384   B=1  S=16384  D=128  bf16 N(0,1)/sqrt(128)  seed 4
+  decode_b32_d128, verify_b8_d128: the two paged workloads at D=128
 
 Paged draw order: context lengths, block permutation, q, K pool, V pool.
 Physical block ids are a random permutation of the pool, dealt to the
@@ -128,6 +129,16 @@ def verify_b8(device="cpu") -> PagedCase:
     return paged_case("verify_b8", 8, 5, 1024, 8192, 64, torch.bfloat16, 3, device=device)
 
 
+def decode_b32_d128(device="cpu") -> PagedCase:
+    """decode_b32 with head_dim 128, the head size of most current models."""
+    return paged_case("decode_b32_d128", 32, 1, 256, 4096, 128, torch.float16, 2, device=device)
+
+
+def verify_b8_d128(device="cpu") -> PagedCase:
+    """verify_b8 with head_dim 128."""
+    return paged_case("verify_b8_d128", 8, 5, 1024, 8192, 128, torch.bfloat16, 3, device=device)
+
+
 def prefill_s16384(device="cpu") -> PrefillCase:
     return prefill_case("prefill_s16384", 1, 16384, 128, torch.bfloat16, 1.0 / math.sqrt(128), 4, device)
 
@@ -138,4 +149,6 @@ WORKLOADS = {
     "decode_b32": decode_b32,
     "verify_b8": verify_b8,
     "prefill_s16384": prefill_s16384,
+    "decode_b32_d128": decode_b32_d128,
+    "verify_b8_d128": verify_b8_d128,
 }

@@ -53,6 +53,14 @@ def test_workload_verify_b8():
     assert_close(out, ref, 1e-2, "verify_b8")
 
 
+@pytest.mark.parametrize("name,tol", [("decode_b32_d128", 2e-3), ("verify_b8_d128", 1e-2)])
+def test_workloads_at_head_dim_128(name, tol):
+    c = workloads.WORKLOADS[name]()
+    out = run(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens)
+    ref = paged_attention_ref(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens, causal=True)
+    assert_close(out, ref, tol, name)
+
+
 @pytest.mark.parametrize("bs", [1, 3, 8, 16, 32])
 @pytest.mark.parametrize("D", [16, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -34,7 +34,7 @@ def _both(q, kp, vp, bt, lt, **kw):
     return plain.cpu(), planned.cpu(), pl
 
 
-@pytest.mark.parametrize("name", ["decode_b32", "verify_b8"])
+@pytest.mark.parametrize("name", ["decode_b32", "verify_b8", "decode_b32_d128", "verify_b8_d128"])
 def test_workloads_planned_equal_unplanned(name):
     from benchmarks import workloads
 
