@@ -89,7 +89,12 @@ struct PagedParams {
 constexpr int kPagedTile = 32;         // tokens per tile
 constexpr int kPagedIds = 384;         // block ids of one workgroup's range staged in LDS
 constexpr int kPagedEntries = 32;      // sequences one workgroup's range may touch
-constexpr int kPagedMaxWaves = 8;      // waves per workgroup
+constexpr int kPagedMaxWaves = 8;      // waves per workgroup (head_dim 256: paged_max_waves)
+// Waves per paged workgroup at head_dim D. At D = 256 a wave's accumulators
+// and q fragments need more than the 256 registers it has when two waves
+// share a SIMD, so those workgroups have at most four waves (one per SIMD)
+// and at most 128 query rows per kv head.
+__host__ __device__ constexpr int paged_max_waves(int D) { return D == 256 ? 4 : kPagedMaxWaves; }
 constexpr int kPagedCUs = 256;         // compute units the launch is sized for
 constexpr int kPagedLdsBudget = 150 * 1024;
 

@@ -155,7 +155,7 @@ __device__ __forceinline__ void store_row(uint16_t* row, const f32x16* acc, floa
 // APPEND: the fused-append variant (p.kn set), a separate instantiation so
 // the plain kernel carries none of its registers or branches.
 template <int DTYPE, int D, bool APPEND>
-__global__ __launch_bounds__(64 * kPagedMaxWaves) void paged_fwd_kernel(const PagedParams p) {
+__global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(const PagedParams p) {
   using C = PagedCfg<D>;
   using E = Elt<DTYPE>;
   extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
@@ -806,13 +806,15 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
   g.R = (Hq / Hk) * Lq;
   g.n_qt = (g.R + 31) / 32;
   g.Rt = std::min(32, g.R);
-  if (g.n_qt > kPagedMaxWaves) {
-    g.err = "more than 256 query rows per kv head (num_heads / num_kv_heads * new tokens)";
+  const int maxw = paged_max_waves(D);
+  if (g.n_qt > maxw) {
+    g.err = D == 256 ? "more than 128 query rows per kv head (num_heads / num_kv_heads * new tokens) at head_dim 256"
+                     : "more than 256 query rows per kv head (num_heads / num_kv_heads * new tokens)";
     return g;
   }
   g.Hg = 1;
   for (int h = 1; h <= Hk; ++h)
-    if (Hk % h == 0 && h * D <= 256 && h * g.n_qt <= kPagedMaxWaves) g.Hg = h;
+    if (Hk % h == 0 && h * D <= 256 && h * g.n_qt <= maxw) g.Hg = h;
   g.NG = Hk / g.Hg;
   g.NWV = g.Hg * g.n_qt;
   g.NCH = g.Hg * D / 8;

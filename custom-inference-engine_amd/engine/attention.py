@@ -167,6 +167,14 @@ class PagedPlan:
     key: tuple
 
 
+def paged_max_rows(head_dim: int) -> int:
+    """Query rows per kv head ((num_heads / num_kv_heads) x new tokens) that
+    one paged launch takes: 256, or 128 at head_dim 256 (a workgroup holds
+    up to 8 waves of 32 rows, 4 at head_dim 256, whose waves need the whole
+    register file of a SIMD)."""
+    return 128 if head_dim == 256 else 256
+
+
 def paged_plan_ints(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size: int, max_blocks_per_seq: int,
                     max_context: int | None = None) -> int:
     """int32 elements of a plan for this launch shape (0 if unsupported)."""

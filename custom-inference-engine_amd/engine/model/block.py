@@ -13,12 +13,12 @@ each, with RoPE fused into the kernels when the model's tables are given:
 * a prefill of fresh sequences (every history is just the new tokens):
   one rotary append that also returns the rotated K densely, then prefill
   attention over the new tokens with q rotated as it is loaded;
-* decode / verify ((Hq/Hk) * L <= 256 query rows per kv head): one rotary
-  append, then paged attention reading K/V in place with q rotated as it
-  is loaded;
-* a long chunk on top of a history (more than 256 query rows per kv
-  head): the rotary append, then paged attention in launches of at most 256
-  rows per kv head (see below) -- the history is never gathered.
+* decode / verify ((Hq/Hk) * L <= 256 query rows per kv head, 128 at
+  head_dim 256: ``paged_max_rows``): one rotary append, then paged attention
+  reading K/V in place with q rotated as it is loaded;
+* a long chunk on top of a history (more query rows per kv head): the rotary
+  append, then paged attention in launches of at most that many rows per kv
+  head (see below) -- the history is never gathered.
 
 :func:`attention_section_rows` takes a ragged step (a different number of
 new tokens per sequence, e.g. a prefill chunk next to decode tokens) as
@@ -41,10 +41,8 @@ import math
 
 import torch
 
-from engine.attention import flash_attention, paged_attention
+from engine.attention import flash_attention, paged_attention, paged_max_rows
 from engine.cache import PagedKVCache, StepBatch
-
-_PAGED_MAX_ROWS = 256  # query rows per kv head one paged launch takes
 
 
 def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_idx: int, cache: PagedKVCache,
@@ -88,13 +86,13 @@ def attention_section(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_i
             cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope, k_out=k_rot)
             flash_attention(q, k_rot.view(B, L, Hk, D).transpose(1, 2), v, causal=True, scale=scale, rope=rope,
                             out=out)  # positions 0..L-1
-    elif (Hq // Hk) * L <= _PAGED_MAX_ROWS and fuse_append and step.aligned:
+    elif (Hq // Hk) * L <= paged_max_rows(D) and fuse_append and step.aligned:
         cache._validate(k_rows)
         cache._validate(v_rows)
         paged_attention(q, cache.k[layer_idx], cache.v[layer_idx], step.block_tables, step.context_lens,
                         causal=True, scale=scale, max_context=step.max_context, rope=rope, out=out,
                         new_kv=(k_rows, v_rows), plan=step.plan_for(True))
-    elif (Hq // Hk) * L <= _PAGED_MAX_ROWS:
+    elif (Hq // Hk) * L <= paged_max_rows(D):
         cache.append_step(layer_idx, step, k_rows, v_rows, rope=rope)
         q_rope = rope
         if rope is not None and not step.aligned:
@@ -123,7 +121,8 @@ def attention_section_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, la
     when ``rope`` is given. ``step`` is ``cache.prepare_step(tables,
     counts)``. Returns (T, Hq * D), row for row. One append for every
     sequence, then paged attention per group of sequences with equal
-    counts, in launches of at most 256 query rows per kv head."""
+    counts, in launches of at most ``paged_max_rows(D)`` query rows per kv
+    head."""
     T, Hq, D = q.shape
     Hk = k.shape[1]
     if T != step.total_new or k.shape[0] != T or v.shape[0] != T or k.shape[1:] != (Hk, D) \
@@ -141,7 +140,7 @@ def _paged_rows(q_rows: torch.Tensor, layer_idx: int, cache: PagedKVCache, step:
     """Paged attention of the packed new-token rows of ``step`` (already
     appended) over each sequence's history, into ``out_rows`` (T, Hq, D).
     Sequences are grouped by their count of new tokens; a group's tokens go
-    in chunks of at most ``_PAGED_MAX_ROWS // (Hq / Hk)`` per launch, chunk
+    in chunks of at most ``paged_max_rows(D) // (Hq / Hk)`` per launch, chunk
     [i0, i1) as the newest tokens of a context of length ctx - count + i1.
     The device index tensors of each launch are built on the first call of
     the step and reused by every layer."""
@@ -160,7 +159,7 @@ def _paged_rows(q_rows: torch.Tensor, layer_idx: int, cache: PagedKVCache, step:
         q_rows = rope_apply(q_rows.transpose(0, 1).unsqueeze(0), rope[0], rope[1],
                             positions=step.cache[key])[0].transpose(0, 1)
         rope = None
-    chunk = max(1, _PAGED_MAX_ROWS // (Hq // Hk))
+    chunk = max(1, paged_max_rows(D) // (Hq // Hk))
     key = ("launches", chunk)
     if key not in step.cache:
         step.cache[key] = _launches(step, chunk, dev)

@@ -110,7 +110,7 @@ size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D,
  * A block id outside [0, num_blocks) or a context length outside
  * [0, min(max_context, max_blocks_per_seq * block_size)] is never
  * dereferenced: the affected sequence's output is written as NaN instead.
- * (Hq / Hk) * Lq must be at most 256. workspace: at least
+ * (Hq / Hk) * Lq must be at most 256 (128 at D = 256). workspace: at least
  * cie_paged_workspace_bytes bytes, 16-byte aligned. Two kernels are launched
  * on the stream: the main pass and the merge of split sequences.
  */

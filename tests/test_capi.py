@@ -162,6 +162,10 @@ def test_paged_workspace_size():
     # more than 256 query rows per kv head is not supported
     assert lib.cie_paged_workspace_bytes(2, 32, 8, 65, 64, 4096, 16, 256) == 0
     assert _paged(Lq=65) == _lib.CIE_EINVAL
+    # at head_dim 256, more than 128
+    assert lib.cie_paged_workspace_bytes(2, 32, 8, 32, 256, 4096, 16, 256) > 0
+    assert lib.cie_paged_workspace_bytes(2, 32, 8, 33, 256, 4096, 16, 256) == 0
+    assert _paged(Lq=33, D=256, qs=_st(8448 * 4, 8448, 256, 1), os_=_st(8448 * 4, 8448, 256, 1)) == _lib.CIE_EINVAL
 
 
 def test_error_codes_map_to_reference_exception_types():

@@ -22,10 +22,11 @@ TILE = 32
 
 def _geometry(Hq, Hk, Lq, D):
     """Head grouping of the launch: the largest divisor Hg of Hk with
-    Hg * D <= 256 and Hg * query tiles <= 8 waves; NG = Hk / Hg groups."""
+    Hg * D <= 256 and Hg * query tiles <= 8 waves (4 at D = 256); NG = Hk / Hg groups."""
     R = (Hq // Hk) * Lq
     n_qt = -(-R // 32)
-    Hg = max(h for h in range(1, Hk + 1) if Hk % h == 0 and h * D <= 256 and h * n_qt <= 8)
+    maxw = 4 if D == 256 else 8
+    Hg = max(h for h in range(1, Hk + 1) if Hk % h == 0 and h * D <= 256 and h * n_qt <= maxw)
     return Hk // Hg
 
 
@@ -186,3 +187,4 @@ def test_plan_argument_errors():
     assert lib.cie_paged_plan(out.data_ptr(), n * 4, lens.data_ptr(), bt.data_ptr(), 4, 2, 8, 3, 1, 64, 10, 16, 4,
                               0, 0) == _lib.CIE_EINVAL
     assert paged_plan_ints(2, 8, 2, 65 * 4, 64, 16, 4) == 0  # more than 256 query rows per kv head
+    assert paged_plan_ints(2, 8, 2, 33, 256, 16, 4) == 0  # more than 128 at head_dim 256

@@ -8,7 +8,8 @@ whole history, causal attention with scale 1/sqrt(D)).
   with and without the model's RoPE tables, and with the new tokens written
   below a sequence's end (positions that differ from context_len - c + i);
 * attention_section with L new tokens per sequence over a history and more
-  than 256 query rows per kv head (the split launches).
+  query rows per kv head than one paged launch takes (256; 128 at head_dim
+  256): the split launches.
 
 PagedKVCache.gather is replaced by a function that raises, so a path that
 falls back to gathering the history fails."""
@@ -110,10 +111,13 @@ def test_ragged_step_matches_reference_order(dtype, rope, below_end, no_gather):
 
 
 @pytest.mark.parametrize("L,Hq,Hk,D,dtype", [(96, 8, 2, 64, torch.float16), (300, 4, 4, 128, torch.bfloat16),
-                                            (257, 2, 2, 32, torch.float16)])
+                                            (257, 2, 2, 32, torch.float16), (40, 8, 2, 256, torch.float16)])
 def test_long_uniform_step_over_history_matches_reference_order(L, Hq, Hk, D, dtype, no_gather):
-    """(Hq/Hk) * L > 256: attention_section splits the chunk into launches."""
-    assert (Hq // Hk) * L > 256
+    """(Hq/Hk) * L above paged_max_rows(D) (256; 128 at head_dim 256):
+    attention_section splits the chunk into launches."""
+    from engine.attention import paged_max_rows
+
+    assert (Hq // Hk) * L > paged_max_rows(D)
     hist = [200, 31, 1000]
     g = torch.Generator().manual_seed(L)
     cache, tables = _cache(Hk, D, dtype, hist, g)
