@@ -41,6 +41,9 @@
 //
 // The tile loop is unrolled by a multiple of the ring depth so that every
 // LDS stage offset is an immediate of the fragment reads.
+//
+// head_dim 128 runs flash_fwd_il_kernel below instead: same tiles and
+// softmax rules, its MFMA and VALU work issued as one interleaved stream.
 #include <type_traits>
 #include <utility>
 
@@ -86,10 +89,7 @@ struct FlashCfg {
   static constexpr int MT = BN / 32;                               // 32-key score tiles
   static constexpr int TILE = BN * D;                              // elements of one tensor tile
   static constexpr int STAGE = 2 * TILE;                           // K tile, then V tile
-  // pipeline steps per workgroup barrier: two at D=128 (1.1 % faster at
-  // S=16384), one elsewhere (D=64: two were 3 % slower)
-  static constexpr int PAIR = D == 128 ? 2 : 1;
-  static constexpr int NST = D == 256 ? 3 : (PAIR == 2 ? 5 : 4);   // ring stages (see the tile loop)
+  static constexpr int NST = D == 256 ? 3 : 4;                     // ring stages (see the tile loop)
   static constexpr int NW = BN * S / 256;                          // 1 KiB copies per wave per tensor
   static constexpr int PER_TILE = 2 * NW;                          // copies per wave per tile
   static constexpr int OCC = D <= 128 ? 2 : 1;                     // workgroups per CU
@@ -269,19 +269,14 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   };
 
   vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
-  const int pro = min(C::PAIR == 2 ? C::NST - 2 : C::NST - 1, n_tiles);
+  const int pro = min(C::NST - 1, n_tiles);
   for (int t = 0; t < pro; ++t) issue(t);
 
   // Software pipeline: iteration t holds S(t) in registers, computes
   // S(t+1) = K(t+1) Q^T while turning S(t) into P(t), then O += V(t) P(t),
-  // so tiles t and t+1 are read. With PAIR = 2 (D=128, five stages) one barrier
-  // serves two steps: at even t every wave waits for its copies of tiles
-  // t+1 and t+2 (all it has in flight), the barrier publishes them, and the
-  // stages of tiles t-2 and t-1 (finished by every wave once it passes the
-  // barrier) are refilled with tiles t+3 and t+4; tiles t, t+1, t+2 stay
-  // resident for steps t and t+1. With PAIR = 1 (four stages; three at
-  // D=256) each step waits for tile t+1, the barrier publishes it, and the
-  // stage of tile t-1 is refilled.
+  // so tiles t and t+1 are read. Each step (four stages; three at D=256)
+  // waits for tile t+1, the barrier publishes it, and the stage of tile t-1
+  // is refilled.
   f32x16 sc[C::MT];
   if (n_tiles > 0) {
     wait_ahead<C::NST, C::PER_TILE>(pro - 1);
@@ -298,16 +293,9 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   // ring stage of tile t (t % NST). The loop below runs U steps per trip with
   // the two score arrays swapped each step, so the scores are never copied
   // between registers.
-  auto step = [&](auto ST, auto EVEN, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
+  auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
     constexpr int st = decltype(ST)::value, st1 = (st + 1) % C::NST;
-    if constexpr (C::PAIR == 2) {
-      if (decltype(EVEN)::value && t + 1 < n_tiles) {
-        vm_wait<0>();
-        __syncthreads();  // tiles t+1, t+2 resident for all waves; stages of t-2, t-1 free
-        if (t + 3 < n_tiles) issue(t + 3);
-        if (t + 4 < n_tiles) issue(t + 4);
-      }
-    } else if (t + 1 < n_tiles) {
+    if (t + 1 < n_tiles) {
       wait_ahead<C::NST, C::PER_TILE>(min(C::NST - 3, n_tiles - 2 - t));
       __syncthreads();  // tile t+1 resident for all waves; stage of tile t-1 free
       if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
@@ -420,15 +408,14 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     }
   };
   f32x16 sb[C::MT];
-  // steps per trip: stage, score buffer and barrier parity all repeat
+  // steps per trip: stage and score buffer repeat
   constexpr int U = C::NST % 2 == 0 ? C::NST : 2 * C::NST;
   for (int t = 0; t < n_tiles; t += U) {
     static_for<U>([&](auto I) CIE_INLINE {
       constexpr int i = decltype(I)::value;
-      using Even = std::integral_constant<bool, i % 2 == 0>;
       if (t + i < n_tiles) {
-        if constexpr (i % 2 == 0) step(std::integral_constant<int, i % C::NST>{}, Even{}, t + i, sc, sb);
-        else step(std::integral_constant<int, i % C::NST>{}, Even{}, t + i, sb, sc);
+        if constexpr (i % 2 == 0) step(std::integral_constant<int, i % C::NST>{}, t + i, sc, sb);
+        else step(std::integral_constant<int, i % C::NST>{}, t + i, sb, sc);
       }
     });
   }
@@ -454,9 +441,400 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Interleaved kernel (head_dim 128; the configuration also covers 64).
+//
+// Same copies, lazy running max and causal rule as flash_fwd_kernel, with
+// two changes to what a wave issues per tile:
+//  * one pipeline step t issues S(t+1) = K(t+1) Q^T (QK MFMAs), O += V(t-1)
+//    P(t-1) (P.V MFMAs, one tile behind) and the softmax of S(t) (exp2 and
+//    packing on the VALU) as one stream, MFMA and VALU work alternating in a
+//    fixed ratio, so the VALU work of one wave overlaps the MFMAs of both
+//    waves of its SIMD;
+//  * the row sums of the rounded probabilities come from 16x16x32 MFMAs
+//    against a 0/1 pattern (no DOT instruction: those wait for the matrix
+//    pipe), already summed over both lanes of a row.
+// The slow path of the lazy max acts on the rows that triggered it only, so
+// a row's arithmetic does not depend on the other rows of its wave.
+// P.V one tile behind keeps V(t-1) resident one step longer: the ring holds
+// tiles t-1, t, t+1 while step t runs (K(t) for the slow path).
+template <int D>
+struct IlCfg {
+  static constexpr int BM = 128;                 // query rows per workgroup
+  static constexpr int BN = D == 64 ? 64 : 32;   // keys per tile
+  static constexpr int S = D / 8;                // 16-byte chunks per row
+  static constexpr int DT = D / 32;              // 32-row output tiles
+  static constexpr int KK = D / 16;              // MFMA steps over head_dim
+  static constexpr int MT = BN / 32;             // 32-key score tiles
+  static constexpr int NCC = 2 * MT;             // 16-key blocks of P per tile
+  static constexpr int TILE = BN * D;
+  static constexpr int STAGE = 2 * TILE;         // K tile, then V tile
+  static constexpr int NST = 5;                  // ring stages
+  static constexpr int AHEAD = NST - 3;          // tiles in flight behind the one a barrier publishes
+  static constexpr int NW = BN * S / 256;        // 1 KiB copies per wave per tensor
+  static constexpr int PER_TILE = 2 * NW;
+  static constexpr int NQK = KK * MT;            // QK^T MFMAs per tile (plus the -m block)
+  static constexpr int NPV = DT * NCC;           // P.V MFMAs per tile
+  static constexpr int NE = 16 * MT;             // scores per lane per tile
+  static constexpr int EPC = NE / (2 * NQK);     // scores per VALU chunk
+  static_assert(NQK == NPV, "QK and P.V MFMAs alternate one for one");
+  static_assert(EPC >= 1 && EPC * 2 * NQK == NE, "softmax chunks must split evenly");
+  static_assert(NW * 256 == BN * S, "tile must split evenly over 4 waves");
+};
+
+// vm_wait for the copies of k tiles (0 <= k <= KMAX) issued after the one needed.
+template <int PER_TILE, int KMAX>
+__device__ __forceinline__ void wait_tiles(int k) {
+  if constexpr (KMAX >= 2) {
+    if (k >= 2) {
+      vm_wait<2 * PER_TILE>();
+      return;
+    }
+  }
+  if constexpr (KMAX >= 1) {
+    if (k == 1) {
+      vm_wait<PER_TILE>();
+      return;
+    }
+  }
+  vm_wait<0>();
+}
+
+template <int DTYPE, int D>
+__global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams p) {
+  using C = IlCfg<D>;
+  using E = Elt<DTYPE>;
+  constexpr int BN = C::BN;
+  __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
+
+  const int N = p.n_wg;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int logical = xcd * (N >> 3) + min(xcd, N & 7) + slot;
+  const int G = p.group;
+  const int per_grp = p.n_mt * G;
+  const int grp = logical / per_grp;
+  const int rem = logical - grp * per_grp;
+  const int mt = p.n_mt - 1 - rem / G;
+  const int g = rem - (rem / G) * G;
+  const int b = grp / p.Hk, kvh = grp - b * p.Hk, hq = kvh * G + g;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int q0w = mt * C::BM + wave * 32;
+  const int qi = q0w + l32;
+
+  const uint16_t* qrow = p.q + b * p.qs0 + hq * p.qs1 + (int64_t)qi * p.qs2;
+  u32x4 qf[C::KK];
+#pragma unroll
+  for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
+  if (p.rope.cos) rope_q_lane<DTYPE, D>(qf, p.rope, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq, hl);
+  {
+    const float c = p.scale_log2;
+    const float cq = p.q_sign ? -c : c;
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const f32x2 v = unpack2<DTYPE>(qf[kk][w]);
+        qf[kk][w] = E::pack2(v[0] * cq, v[1] * cq);
+      }
+  }
+
+  const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;
+  int kend = p.Lk;
+  if (p.causal) kend = max(0, min(p.Lk, p.Lk - p.Lq + wg_last_row + 1));
+  int wave_kend = 0;
+  if (q0w < p.Lq) {
+    wave_kend = p.Lk;
+    if (p.causal) wave_kend = max(0, min(p.Lk, p.Lk - p.Lq + min(q0w + 31, p.Lq - 1) + 1));
+  }
+  const int lim = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + qi) : p.Lk - 1;
+  const int wave_lim0 = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + q0w) : p.Lk - 1;
+  const int n_tiles = (kend + BN - 1) / BN;
+  const int wave_nt = (wave_kend + BN - 1) / BN;  // tiles this wave needs (0: no rows)
+
+  const uint16_t* kb = p.k + b * p.ks0 + kvh * p.ks1;
+  const uint16_t* vb = p.v + b * p.vs0 + kvh * p.vs1;
+  const int last_key = max(p.Lk - 1, 0);
+
+  int lrow[C::NW], lchk[C::NW];
+#pragma unroll
+  for (int j = 0; j < C::NW; ++j) {
+    const int P = (wave * C::NW + j) * 64 + lane;
+    lrow[j] = P / C::S;
+    lchk[j] = 8 * ((P % C::S) ^ chunk_swizzle<C::S>(lrow[j]));
+  }
+  const bool off32 = (int64_t)BN * max(p.ks2, p.vs2) * 2 + 2 * D < ((int64_t)1 << 31);
+  uint32_t koff[C::NW], voff[C::NW];
+#pragma unroll
+  for (int j = 0; j < C::NW; ++j) {
+    koff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.ks2 + lchk[j])) : 0u;
+    voff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.vs2 + lchk[j])) : 0u;
+  }
+  const uint32_t ring_lds = lds_addr_of(ring);
+  auto issue = [&](int t) CIE_INLINE {
+    const int n0 = t * BN;
+    const uint32_t st = ring_lds + 2u * (uint32_t)((t % C::NST) * C::STAGE + wave * C::NW * 512);
+    if (off32 && n0 + BN <= p.Lk) {
+      const void* kt = uniform_ptr(kb + (int64_t)n0 * p.ks2);
+      const void* vt = uniform_ptr(vb + (int64_t)n0 * p.vs2);
+#pragma unroll
+      for (int j = 0; j < C::NW; ++j) {
+        dma16_sv(kt, koff[j], st + 1024u * j);
+        dma16_sv(vt, voff[j], st + 2u * C::TILE + 1024u * j);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::NW; ++j) {
+        const int key = min(n0 + lrow[j], last_key);
+        dma16_at(kb + (int64_t)key * p.ks2 + lchk[j], st + 1024u * j);
+        dma16_at(vb + (int64_t)key * p.vs2 + lchk[j], st + 2u * C::TILE + 1024u * j);
+      }
+    }
+  };
+
+  // K fragment (head_dim step kk, 32-key score tile mt2) of the tile in stage ks.
+  auto kfrag = [&](const uint16_t* ks, int kk, int mt2) CIE_INLINE {
+    const int row = 32 * mt2 + l32;
+    const int sl = (2 * kk + hl) ^ chunk_swizzle<C::S>(row);
+    return *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
+  };
+  // S^T of the tile in stage ks (no -m block).
+  auto qk = [&](const uint16_t* ks, f32x16* s) CIE_INLINE {
+#pragma unroll
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk)
+#pragma unroll
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = E::mfma(kfrag(ks, kk, mt2), qf[kk], s[mt2]);
+  };
+  // Element e of score tile mt2 in a lane is key n0 + 32 mt2 + 4 hl + 8 (e / 4)
+  // + e % 4: the test key <= lim compares one per-lane value with a constant.
+  auto mask = [&](int t, f32x16* s) CIE_INLINE {
+    const int n0 = t * BN;
+    if (n0 + BN - 1 > wave_lim0) {
+      const int r = lim - n0 - 4 * hl;
+#pragma unroll
+      for (int mt2 = 0; mt2 < C::MT; ++mt2)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[mt2][e] = 32 * mt2 + 8 * (e >> 2) + (e & 3) <= r ? s[mt2][e] : -INFINITY;
+    }
+  };
+  auto rowmax = [&](const f32x16* s) CIE_INLINE {
+    float mx = max16(s[0]);
+#pragma unroll
+    for (int mt2 = 1; mt2 < C::MT; ++mt2) mx = maxf(mx, max16(s[mt2]));
+    return xhalf_max(mx);
+  };
+  // V^T fragment (output tile dt, 16-key block cc) of the tile in stage vs.
+  const int rq = lane & 15, gq = lane >> 4;
+  auto vfrag = [&](const uint16_t* vs, int dt, int cc) CIE_INLINE {
+    const int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
+    const int chunk = d >> 3, within = d & 7;
+    const int tlo = 16 * cc + 4 * hl + (rq >> 2);
+    const int thi = tlo + 8;
+    const u32x2 lo = lds_read_tr16(vs + (tlo * C::S + (chunk ^ chunk_swizzle<C::S>(tlo))) * 8 + within);
+    const u32x2 hi = lds_read_tr16(vs + (thi * C::S + (chunk ^ chunk_swizzle<C::S>(thi))) * 8 + within);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+
+  f32x16 acc[C::DT];
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
+  float m = -INFINITY, l = 0.f;  // l: the row's sum over both lanes
+  uint32_t bm = 0u;  // word 0 of the -m block's B operand
+  constexpr float kMScale = DTYPE == 0 ? 256.f : 1.f;  // fp16 range for |m| up to 2^24
+  const u32x4 a_one = {hl == 0 ? E::pack2(kMScale, 0.f) : 0u, 0u, 0u, 0u};
+  auto set_m = [&](float x) CIE_INLINE {  // m = x rounded to what the B operand holds exactly
+    if (x != -INFINITY) {
+      x = fminf(x, 65504.f * kMScale);
+      x = unpack2<DTYPE>(E::pack2(x * (1.f / kMScale), 0.f))[0] * kMScale;
+    }
+    m = x;
+    bm = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
+  };
+  // Row-sum pattern of the 16x16x32 MFMA: A[i][k] = 1 iff bit 3 of k equals
+  // bit 2 of i. With P^T of a 16-key block as B (lane L: row L % 32, keys
+  // 8 (L / 32) ..), every element of lane L of the result is the block's sum
+  // over row L % 32.
+  const uint32_t sel = ((lane >> 4) & 1) == ((lane >> 2) & 1) ? E::pack2(1.f, 1.f) : 0u;
+  const u32x4 a_sum = {sel, sel, sel, sel};
+
+  vm_wait<0>();  // q (and RoPE tables) in registers before the copies start
+  const int pro = min(C::AHEAD + 1, n_tiles);
+  for (int t = 0; t < pro; ++t) issue(t);
+
+  f32x16 sA[C::MT], sB[C::MT];
+  u32x4 pA[C::NCC], pB[C::NCC];
+  if (n_tiles > 0) {
+    wait_tiles<C::PER_TILE, C::AHEAD>(pro - 1);
+    __syncthreads();
+    qk(ring, sA);
+    mask(0, sA);
+    set_m(rowmax(sA));  // the reference max starts at tile 0's row max
+    const float sub = m == -INFINITY ? 0.f : m;
+#pragma unroll
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) sA[mt2] -= sub;
+  }
+
+  // Lazy-max check of tile tc (its P in pq, its row sum of p in every
+  // element of tsum; K(tc) in stage kst; sx = S(tc+1) - m). A row whose sum
+  // passed 2^10 (some p may not fit the 16-bit P.V operand; always the case
+  // for a row that had no visible key before) recomputes S(tc) from the
+  // resident K tile, raises m to its row max, rescales O and l, and redoes
+  // its p; the other rows keep theirs.
+  auto check = [&](const int tc, const uint16_t* kst, u32x4* pq, f32x16* sx, f32x4 tsum) CIE_INLINE {
+    const bool trig = !(tsum[0] <= kSumTrigger);
+    if (__builtin_amdgcn_ballot_w64(trig)) {
+      f32x16 s2[C::MT];
+      qk(kst, s2);
+      mask(tc, s2);
+      const float mx = rowmax(s2);
+      const float m_old = m;
+      if (trig) set_m(maxf(m_old, mx));
+      const float alpha = m > m_old ? exp2_fast(m_old - m) : 1.f;  // 0 when m was -inf
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
+      const float nm = m == -INFINITY ? 0.f : -m;
+      const float adj = (m_old == -INFINITY ? 0.f : m_old) + nm;  // 0 for rows that keep m
+#pragma unroll
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) sx[mt2] += adj;
+#pragma unroll
+      for (int e = 0; e < C::NE; e += 2) {
+        const int m2 = e / 16, ee = e % 16;
+        const uint32_t w = pq[2 * m2 + (ee >> 3)][(ee & 7) >> 1];
+        pq[2 * m2 + (ee >> 3)][(ee & 7) >> 1] =
+            trig ? E::pack2(exp2_fast(s2[m2][ee] + nm), exp2_fast(s2[m2][ee + 1] + nm)) : w;
+      }
+      f32x4 ts2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < C::NCC; ++cc) ts2 = E::mfma16(a_sum, pq[cc], ts2);
+      if (trig) tsum = ts2;
+    }
+    l += tsum[0];
+  };
+
+  // One pipeline step t: ST = t % NST, PV = t > 0. sc = S(t) - m, sn
+  // receives S(t+1) - m, pb receives P(t), pp holds P(t-1).
+  auto step = [&](auto ST, auto PV, const int t, f32x16* sc, f32x16* sn, u32x4* pb, u32x4* pp) CIE_INLINE {
+    constexpr int st = decltype(ST)::value;
+    constexpr int st1 = (st + 1) % C::NST, stp = (st + C::NST - 1) % C::NST;
+    constexpr bool has_pv = decltype(PV)::value;
+    if (t + 1 < n_tiles) {
+      // tile t+1 resident for all waves; the stage of tile t-2 is free (its
+      // last reads were in step t-1)
+      wait_tiles<C::PER_TILE, C::AHEAD - 1>(min(n_tiles - 1, t + C::AHEAD) - (t + 1));
+      __syncthreads();
+      if (t + C::AHEAD + 1 < n_tiles) issue(t + C::AHEAD + 1);
+    }
+    // A wave works on tiles [0, wave_nt); step wave_nt only finishes P.V of
+    // its last tile (its S(t) is fully masked: p = 0).
+    if (wave_nt == 0 || t > wave_nt) return;
+
+    const uint16_t* ks = ring + st1 * C::STAGE;
+    const uint16_t* vs = ring + stp * C::STAGE + C::TILE;
+    // Fragments are read LA MFMA pairs ahead of their use.
+    constexpr int LA = 1;
+    u32x4 ka[C::NQK], va[C::NPV];
+    auto fetch = [&](int i) CIE_INLINE {
+      ka[i] = kfrag(ks, i / C::MT, i % C::MT);
+      if constexpr (has_pv) va[i] = vfrag(vs, i % C::DT, i / C::DT);
+    };
+#pragma unroll
+    for (int i = 0; i < LA; ++i) fetch(i);
+#pragma unroll
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = E::mfma(a_one, u32x4{bm, 0u, 0u, 0u}, f32x16{});
+    f32x4 tsum = {0.f, 0.f, 0.f, 0.f};
+    // VALU chunk c: exp2 of scores [c EPC, (c + 1) EPC) of S(t) (score tile
+    // e / 16, element e % 16), pairs packed into P(t); each completed 16-key
+    // block of P(t) is summed by an MFMA.
+    auto chunk = [&](auto CI) CIE_INLINE {
+      constexpr int c0 = decltype(CI)::value;
+#pragma unroll
+      for (int e = c0 * C::EPC; e < (c0 + 1) * C::EPC; ++e) {
+        const int m2 = e / 16, ee = e % 16;
+        sc[m2][ee] = exp2_fast(sc[m2][ee]);
+        if (ee & 1) {
+          const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
+          asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
+          pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
+        }
+        if ((ee & 7) == 7) tsum = E::mfma16(a_sum, pb[e / 8], tsum);
+      }
+    };
+    static_for<C::NQK>([&](auto I) CIE_INLINE {
+      constexpr int i = decltype(I)::value;
+      if constexpr (i + LA < C::NQK) fetch(i + LA);
+      sn[i % C::MT] = E::mfma(ka[i], qf[i / C::MT], sn[i % C::MT]);
+      __builtin_amdgcn_sched_barrier(0);
+      chunk(std::integral_constant<int, 2 * i>{});
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (has_pv) acc[i % C::DT] = E::mfma(va[i], pp[i / C::DT], acc[i % C::DT]);
+      __builtin_amdgcn_sched_barrier(0);
+      chunk(std::integral_constant<int, 2 * i + 1>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    check(t, ring + st * C::STAGE, pb, sn, tsum);
+    mask(t + 1, sn);
+  };
+
+  if (n_tiles > 0) step(std::integral_constant<int, 0>{}, std::false_type{}, 0, sA, sB, pA, pB);
+  constexpr int U = 2 * C::NST;  // stage and buffer parity repeat
+  for (int t = 1; t < n_tiles; t += U) {
+    static_for<U>([&](auto I) CIE_INLINE {
+      constexpr int i = decltype(I)::value;
+      constexpr int st = (1 + i) % C::NST;
+      if (t + i < n_tiles) {
+        if constexpr ((1 + i) % 2 == 1)
+          step(std::integral_constant<int, st>{}, std::true_type{}, t + i, sB, sA, pB, pA);
+        else
+          step(std::integral_constant<int, st>{}, std::true_type{}, t + i, sA, sB, pA, pB);
+      }
+    });
+  }
+  // P.V of the last tile when no further step ran it.
+  if (wave_nt > 0 && wave_nt == n_tiles) {
+    const int tl = n_tiles - 1;
+    const uint16_t* vs = ring + (tl % C::NST) * C::STAGE + C::TILE;
+    auto fin = [&](const u32x4* pq) CIE_INLINE {
+      u32x4 va[C::NPV];
+#pragma unroll
+      for (int i = 0; i < C::NPV; ++i) va[i] = vfrag(vs, i % C::DT, i / C::DT);
+#pragma unroll
+      for (int i = 0; i < C::NPV; ++i) acc[i % C::DT] = E::mfma(va[i], pq[i / C::DT], acc[i % C::DT]);
+    };
+    if (tl & 1) fin(pB);
+    else fin(pA);
+  }
+
+  // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
+  // reference's softmax over an all -inf row; Lk == 0 gives zeros.
+  const float inv = p.Lk == 0 ? 0.f : 1.f / l;
+  if (qi < p.Lq) {
+    uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)qi * p.os2;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * dt + 8 * g4 + 4 * hl;
+        const u32x2 w = {E::pack2(acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv),
+                         E::pack2(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+    }
+  }
+}
+
+// head_dim 128 runs the interleaved kernel (S=16384 bf16 causal: 1863 ->
+// 1774 us); at head_dim 64 it measured 2 % slower than flash_fwd_kernel, whose
+// VALU-heavy and MFMA-only phases the other wave of each SIMD pairs up.
 template <int DTYPE, int D>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+  if constexpr (D == 128)
+    hipLaunchKernelGGL((flash_fwd_il_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
