@@ -30,14 +30,15 @@
 // Q is scaled by c once, as it is loaded, and rounded to the input type
 // (relative error 2^-11 for fp16, 2^-8 for bf16 per element, far inside the
 // output tolerances; c * q must be finite in the input type); m is kept at a
-// value the 16-bit B operand holds exactly. The running max is refreshed lazily and without a per-tile row
-// max: p(t) is computed against the reference max m, and only when a lane's 32
-// probabilities of the tile sum past 2^10 (so some p may not fit the 16-bit
-// P.V operand; always the case for a row that had no visible key before)
-// does the wave recompute S(t) from the still-resident K tile, take its row
-// max, raise m to it and redo the tile. Otherwise every p <= 2^10, exact to
-// fp16 / bf16 rounding. The final acc / l is unchanged by the choice of m.
-// l accumulates the probabilities as rounded for the P.V product.
+// value the 16-bit B operand holds exactly. The running max is refreshed
+// lazily and without a per-tile row max: p(t) is computed against the
+// reference max m, and only when a row's probabilities of the tile sum past
+// 2^10 (so some p may not fit the 16-bit P.V operand; always the case for a
+// row that had no visible key before) does the wave recompute S(t) from the
+// still-resident K tile, take its row max, raise m to it and redo the tile.
+// Otherwise every p <= 2^10, exact to fp16 / bf16 rounding. The final acc / l
+// is unchanged by the choice of m. l accumulates the probabilities as rounded
+// for the P.V product, summed by 16x16x32 MFMAs (see a_sum).
 //
 // The tile loop is unrolled by a multiple of the ring depth so that every
 // LDS stage offset is an immediate of the fragment reads.
@@ -267,6 +268,12 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     m = x;
     b_m[0] = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
   };
+  // Row-sum pattern of the 16x16x32 MFMA: A[i][k] = 1 iff bit 3 of k equals
+  // bit 2 of i. With P^T of a 16-key block as B (lane L: row L % 32, keys
+  // 8 (L / 32) ..), every element of lane L of the result is the block's sum
+  // over row L % 32 (both lanes of the row).
+  const uint32_t sel1 = ((lane >> 4) & 1) == ((lane >> 2) & 1) ? E::pack2(1.f, 1.f) : 0u;
+  const u32x4 a_sum = {sel1, sel1, sel1, sel1};
 
   vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
   const int pro = min(C::NST - 1, n_tiles);
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // wave's P.V phase fills the gaps (measured 4-5 % faster at D=64).
     __builtin_amdgcn_s_setprio(1);
     u32x4 pb[2 * C::MT];
-    float ts0 = 0.f, ts1 = 0.f;  // this lane's sum of the tile's p (two chains)
+    f32x4 tsm = {0.f, 0.f, 0.f, 0.f};  // the tile's row sum of p (every element)
     {
       const uint16_t* ks = ring + st1 * C::STAGE;
       u32x4 ka[C::NQK];
@@ -336,13 +343,14 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
         for (int e = i * EPC; e < (i + 1) * EPC; ++e) {
           const int m2 = e / 16, ee = e % 16;
           sc[m2][ee] = exp2_fast(sc[m2][ee]);
-          if (ee & 1) {  // a pair is complete: pack it and add it to the row sum
+          if (ee & 1) {  // a pair is complete: pack it
             const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
             asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
             pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
-            if (ee & 2) ts1 = E::sum2(pk, ts1);
-            else ts0 = E::sum2(pk, ts0);
           }
+          // a 16-key block of P(t) is complete: its row sum on the matrix pipe
+          // (a DOT instruction per pair would wait for the pipe to drain)
+          if ((ee & 7) == 7) tsm = E::mfma16(a_sum, pb[2 * m2 + (ee >> 3)], tsm);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -353,7 +361,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // Slow path of the lazy max (rare: a row's max rose by ~2^5 or more, or
     // its first visible key): S(t) again from the resident K tile, m raised
     // to the row max, accumulators rescaled, the tile's p recomputed.
-    float ts = ts0 + ts1;
+    float ts = tsm[0];
     if (__builtin_amdgcn_ballot_w64(!(ts <= kSumTrigger))) {
       const float m_in = m == -INFINITY ? 0.f : m;  // subtracted from S(t+1) in sn
       qk(t, sc);
@@ -367,17 +375,16 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
       const float nm = m == -INFINITY ? 0.f : -m;
 #pragma unroll
       for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] += m_in + nm;
-      ts0 = 0.f;
-      ts1 = 0.f;
 #pragma unroll
       for (int e = 0; e < 16 * C::MT; e += 2) {
         const int m2 = e / 16, ee = e % 16;
-        const uint32_t pk = E::pack2(exp2_fast(sc[m2][ee] + nm), exp2_fast(sc[m2][ee + 1] + nm));
-        pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
-        if (ee & 2) ts1 = E::sum2(pk, ts1);
-        else ts0 = E::sum2(pk, ts0);
+        pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] =
+            E::pack2(exp2_fast(sc[m2][ee] + nm), exp2_fast(sc[m2][ee + 1] + nm));
       }
-      ts = ts0 + ts1;
+      tsm = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < 2 * C::MT; ++cc) tsm = E::mfma16(a_sum, pb[cc], tsm);
+      ts = tsm[0];
     }
     l += ts;
     mask(t + 1, sn);
@@ -422,7 +429,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
   // reference's softmax over an all -inf row; Lk == 0 gives zeros.
-  const float l_tot = xhalf_sum(l);
+  const float l_tot = l;  // the sum MFMAs add both lanes of a row
   const float inv = p.Lk == 0 ? 0.f : 1.f / l_tot;
   if (qi < p.Lq) {
     uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)qi * p.os2;
