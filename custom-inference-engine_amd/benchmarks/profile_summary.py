@@ -35,6 +35,7 @@ XCDS = 8            # accelerator complex dies of one MI355X; GRBM_GUI_ACTIVE is
 SIMDS = 256 * 4     # 256 CUs x 4 SIMDs; SQ_VALU_MFMA_BUSY_CYCLES is summed over them
 COPY_BYTES = 256 << 20
 PROBE_WORKLOADS = {2048: "prefill_s2048", 4096: "prefill_s16384"}
+PREFILL_KERNELS = ("cie::flash_fwd_kernel", "cie::flash_fwd_il_kernel")  # head_dim 128 runs the second
 
 
 def _grid(r: dict) -> tuple[int, int]:
@@ -118,7 +119,7 @@ def _counter_rows(paths: list[str]) -> dict:
 
 
 def mfma(paths: list[str]) -> None:
-    rows = [d for d in _counter_rows(paths).values() if d["name"].startswith("cie::flash_fwd_kernel")]
+    rows = [d for d in _counter_rows(paths).values() if d["name"].startswith(PREFILL_KERNELS)]
     print("| dispatch | workload | us | MFMA instr | MFMA busy / SIMD (cycles) | shader cycles per XCD "
           "| clock GHz | MFMA busy | fp16+bf16 MOPS x 512 (GFLOP) |")
     print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
@@ -147,7 +148,7 @@ def mfma(paths: list[str]) -> None:
     for path in paths:
         seen.clear()
         for d in _counter_rows([path]).values():
-            if not d["name"].startswith("cie::flash_fwd_kernel"):
+            if not d["name"].startswith(PREFILL_KERNELS):
                 continue
             wl = PROBE_WORKLOADS.get(d["grid"][0], "?")
             key = (wl, seen[wl])
