@@ -38,7 +38,7 @@
 // still-resident K tile, take its row max, raise m to it and redo the tile.
 // Otherwise every p <= 2^10, exact to fp16 / bf16 rounding. The final acc / l
 // is unchanged by the choice of m. l accumulates the probabilities as rounded
-// for the P.V product, summed by 16x16x32 MFMAs (see a_sum).
+// for the P.V product, summed on the matrix pipe (see sum_ones).
 //
 // The tile loop is unrolled by a multiple of the ring depth so that every
 // LDS stage offset is an immediate of the fragment reads.
@@ -268,12 +268,11 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     m = x;
     b_m[0] = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
   };
-  // Row-sum pattern of the 16x16x32 MFMA: A[i][k] = 1 iff bit 3 of k equals
-  // bit 2 of i. With P^T of a 16-key block as B (lane L: row L % 32, keys
-  // 8 (L / 32) ..), every element of lane L of the result is the block's sum
-  // over row L % 32 (both lanes of the row).
-  const uint32_t sel1 = ((lane >> 4) & 1) == ((lane >> 2) & 1) ? E::pack2(1.f, 1.f) : 0u;
-  const u32x4 a_sum = {sel1, sel1, sel1, sel1};
+  // Row sums of P: 4x4x4 MFMAs (16 blocks) with A all ones add four packed
+  // p of a lane into that lane's accumulator and nothing else (a p that is
+  // inf or NaN stays in its row); two chains, then one cross-lane add per
+  // tile for the row.
+  const u32x2 sum_ones = {E::pack2(1.f, 1.f), E::pack2(1.f, 1.f)};
 
   vm_wait<0>();  // Q is in registers before the copies start (explicit waits from here on)
   const int pro = min(C::NST - 1, n_tiles);
@@ -320,7 +319,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // wave's P.V phase fills the gaps (measured 4-5 % faster at D=64).
     __builtin_amdgcn_s_setprio(1);
     u32x4 pb[2 * C::MT];
-    f32x4 tsm = {0.f, 0.f, 0.f, 0.f};  // the tile's row sum of p (every element)
+    f32x4 tsm[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // this lane's sums of the tile's p
     {
       const uint16_t* ks = ring + st1 * C::STAGE;
       u32x4 ka[C::NQK];
@@ -348,9 +347,12 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
             asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
             pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
           }
-          // a 16-key block of P(t) is complete: its row sum on the matrix pipe
-          // (a DOT instruction per pair would wait for the pipe to drain)
-          if ((ee & 7) == 7) tsm = E::mfma16(a_sum, pb[2 * m2 + (ee >> 3)], tsm);
+          // four p of P(t) are packed: their sum on the matrix pipe (a DOT
+          // instruction per pair would wait for the pipe to drain)
+          if ((ee & 3) == 3) {
+            const int c = 2 * m2 + (ee >> 3), w = (ee & 7) >> 1;
+            tsm[(ee >> 2) & 1] = E::mfma4(sum_ones, u32x2{pb[c][w - 1], pb[c][w]}, tsm[(ee >> 2) & 1]);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -361,7 +363,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // Slow path of the lazy max (rare: a row's max rose by ~2^5 or more, or
     // its first visible key): S(t) again from the resident K tile, m raised
     // to the row max, accumulators rescaled, the tile's p recomputed.
-    float ts = tsm[0];
+    float ts = xhalf_sum(tsm[0][0] + tsm[1][0]);  // the row's sum of the tile's p
     if (__builtin_amdgcn_ballot_w64(!(ts <= kSumTrigger))) {
       const float m_in = m == -INFINITY ? 0.f : m;  // subtracted from S(t+1) in sn
       qk(t, sc);
@@ -381,10 +383,13 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
         pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] =
             E::pack2(exp2_fast(sc[m2][ee] + nm), exp2_fast(sc[m2][ee + 1] + nm));
       }
-      tsm = f32x4{0.f, 0.f, 0.f, 0.f};
+      tsm[0] = tsm[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int cc = 0; cc < 2 * C::MT; ++cc) tsm = E::mfma16(a_sum, pb[cc], tsm);
-      ts = tsm[0];
+      for (int cc = 0; cc < 2 * C::MT; ++cc) {
+        tsm[0] = E::mfma4(sum_ones, u32x2{pb[cc][0], pb[cc][1]}, tsm[0]);
+        tsm[1] = E::mfma4(sum_ones, u32x2{pb[cc][2], pb[cc][3]}, tsm[1]);
+      }
+      ts = xhalf_sum(tsm[0][0] + tsm[1][0]);
     }
     l += ts;
     mask(t + 1, sn);
@@ -429,7 +434,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
   // reference's softmax over an all -inf row; Lk == 0 gives zeros.
-  const float l_tot = l;  // the sum MFMAs add both lanes of a row
+  const float l_tot = l;  // l sums both lanes of the row
   const float inv = p.Lk == 0 ? 0.f : 1.f / l_tot;
   if (qi < p.Lq) {
     uint16_t* orow = p.o + b * p.os0 + hq * p.os1 + (int64_t)qi * p.os2;
@@ -660,12 +665,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
     m = x;
     bm = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
   };
-  // Row-sum pattern of the 16x16x32 MFMA: A[i][k] = 1 iff bit 3 of k equals
-  // bit 2 of i. With P^T of a 16-key block as B (lane L: row L % 32, keys
-  // 8 (L / 32) ..), every element of lane L of the result is the block's sum
-  // over row L % 32.
-  const uint32_t sel = ((lane >> 4) & 1) == ((lane >> 2) & 1) ? E::pack2(1.f, 1.f) : 0u;
-  const u32x4 a_sum = {sel, sel, sel, sel};
+  // Row sums of P: 4x4x4 MFMAs with A all ones (see flash_fwd_kernel).
+  const u32x2 sum_ones = {E::pack2(1.f, 1.f), E::pack2(1.f, 1.f)};
 
   vm_wait<0>();  // q (and RoPE tables) in registers before the copies start
   const int pro = min(C::AHEAD + 1, n_tiles);
@@ -684,14 +685,14 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
     for (int mt2 = 0; mt2 < C::MT; ++mt2) sA[mt2] -= sub;
   }
 
-  // Lazy-max check of tile tc (its P in pq, its row sum of p in every
-  // element of tsum; K(tc) in stage kst; sx = S(tc+1) - m). A row whose sum
+  // Lazy-max check of tile tc (its P in pq, its row sum of p in ts; K(tc)
+  // in stage kst; sx = S(tc+1) - m). A row whose sum
   // passed 2^10 (some p may not fit the 16-bit P.V operand; always the case
   // for a row that had no visible key before) recomputes S(tc) from the
   // resident K tile, raises m to its row max, rescales O and l, and redoes
   // its p; the other rows keep theirs.
-  auto check = [&](const int tc, const uint16_t* kst, u32x4* pq, f32x16* sx, f32x4 tsum) CIE_INLINE {
-    const bool trig = !(tsum[0] <= kSumTrigger);
+  auto check = [&](const int tc, const uint16_t* kst, u32x4* pq, f32x16* sx, float ts) CIE_INLINE {
+    const bool trig = !(ts <= kSumTrigger);
     if (__builtin_amdgcn_ballot_w64(trig)) {
       f32x16 s2[C::MT];
       qk(kst, s2);
@@ -714,12 +715,16 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
         pq[2 * m2 + (ee >> 3)][(ee & 7) >> 1] =
             trig ? E::pack2(exp2_fast(s2[m2][ee] + nm), exp2_fast(s2[m2][ee + 1] + nm)) : w;
       }
-      f32x4 ts2 = {0.f, 0.f, 0.f, 0.f};
+      f32x4 t2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int cc = 0; cc < C::NCC; ++cc) ts2 = E::mfma16(a_sum, pq[cc], ts2);
-      if (trig) tsum = ts2;
+      for (int cc = 0; cc < C::NCC; ++cc) {
+        t2[0] = E::mfma4(sum_ones, u32x2{pq[cc][0], pq[cc][1]}, t2[0]);
+        t2[1] = E::mfma4(sum_ones, u32x2{pq[cc][2], pq[cc][3]}, t2[1]);
+      }
+      const float ts2 = xhalf_sum(t2[0][0] + t2[1][0]);
+      if (trig) ts = ts2;
     }
-    l += tsum[0];
+    l += ts;
   };
 
   // One pipeline step t: ST = t % NST, PV = t > 0. sc = S(t) - m, sn
@@ -752,10 +757,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
     for (int i = 0; i < LA; ++i) fetch(i);
 #pragma unroll
     for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = E::mfma(a_one, u32x4{bm, 0u, 0u, 0u}, f32x16{});
-    f32x4 tsum = {0.f, 0.f, 0.f, 0.f};
+    f32x4 tsum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     // VALU chunk c: exp2 of scores [c EPC, (c + 1) EPC) of S(t) (score tile
-    // e / 16, element e % 16), pairs packed into P(t); each completed 16-key
-    // block of P(t) is summed by an MFMA.
+    // e / 16, element e % 16), pairs packed into P(t); every four packed p
+    // are summed by an MFMA.
     auto chunk = [&](auto CI) CIE_INLINE {
       constexpr int c0 = decltype(CI)::value;
 #pragma unroll
@@ -767,7 +772,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
           asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
           pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
         }
-        if ((ee & 7) == 7) tsum = E::mfma16(a_sum, pb[e / 8], tsum);
+        if ((ee & 3) == 3) {
+          const int c = 2 * m2 + (ee >> 3), w = (ee & 7) >> 1;
+          tsum[(ee >> 2) & 1] = E::mfma4(sum_ones, u32x2{pb[c][w - 1], pb[c][w]}, tsum[(ee >> 2) & 1]);
+        }
       }
     };
     static_for<C::NQK>([&](auto I) CIE_INLINE {
@@ -782,7 +790,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
       chunk(std::integral_constant<int, 2 * i + 1>{});
       __builtin_amdgcn_sched_barrier(0);
     });
-    check(t, ring + st * C::STAGE, pb, sn, tsum);
+    check(t, ring + st * C::STAGE, pb, sn, xhalf_sum(tsum[0][0] + tsum[1][0]));
     mask(t + 1, sn);
   };
 

@@ -124,12 +124,57 @@ def test_strided_views_match_contiguous():
     assert torch.equal(out, out_c)
 
 
-def test_gqa_equals_expanded_mha_bitwise():
-    q, k, v = _inputs(2, 8, 2, 100, 140, 64, torch.float16, seed=9)
+@pytest.mark.parametrize("D", [64, 128])
+def test_gqa_equals_expanded_mha_bitwise(D):
+    q, k, v = _inputs(2, 8, 2, 100, 140, D, torch.float16, seed=9)
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
     gqa = flash_attention(q, k, v, causal=True)
     mha = flash_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), causal=True)
     assert torch.equal(gqa, mha)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_nan_query_row_stays_in_its_row(D, dtype):
+    """A NaN in one query row makes that row NaN and no other, as the
+    reference's per-row softmax does (the row sums run on the matrix pipe
+    and must not mix rows: rows r and r + 16 of a wave once shared an MFMA
+    column, where 0 x NaN = NaN)."""
+    q, k, v = _inputs(1, 4, 2, 96, 96, D, dtype, seed=23)
+    qn = q.clone()
+    qn[0, 1, 0, 3] = float("nan")
+    qn[0, 2, 37, 0] = float("nan")
+    clean = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    out = flash_attention(qn.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    ref = flash_attention_ref(qn.float(), k.float(), v.float(), causal=True)
+    assert_close(out, ref, TOL[dtype], f"nan rows D={D} {dtype}")  # includes the NaN pattern
+    if D == 128:  # the slow path there acts per row: the other rows keep their bits
+        keep = ~torch.isnan(ref).any(dim=-1)
+        assert torch.equal(out.cpu()[keep], clean.cpu()[keep])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_d128_rows_do_not_depend_on_their_wave(dtype):
+    """head_dim 128: a row whose scores rise across tiles takes the lazy-max
+    slow path; the other rows of its wave (rows 1..31 of the same 32-row
+    strip) keep their arithmetic, so their outputs are bit-identical to a run
+    in which no row of the strip takes it."""
+    D, L = 128, 320
+    g = torch.Generator().manual_seed(21)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    q = torch.randn(1, 2, L, D, generator=g) * 0.3
+    k = torch.randn(1, 1, L, D, generator=g) * 0.3
+    k += (torch.arange(L, dtype=torch.float32) / 32.0 * 20.0 * math.sqrt(D) / (3.0 * math.log2(math.e)))[None, None, :, None] * u
+    v = torch.randn(1, 1, L, D, generator=g) * 0.5
+    quiet = q.clone()
+    loud = q.clone()
+    loud[:, :, 0] += 3.0 * u  # row 0 (and its wave's slow path) rises with the keys
+    outs = [flash_attention(x.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=False)
+            for x in (quiet, loud)]
+    assert torch.equal(outs[0][:, :, 1:32], outs[1][:, :, 1:32])
+    ref = flash_attention_ref(loud.to(dtype).float(), k.to(dtype).float(), v.to(dtype).float(), causal=False)
+    assert_close(outs[1], ref, TOL[dtype], f"loud row {dtype}")
 
 
 @pytest.mark.parametrize("D", [64, 128])
