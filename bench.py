@@ -609,8 +609,11 @@ def main():
     case = workloads.prefill_s2048()
     q, k, v = case.q.to(dev), case.k.to(dev), case.v.to(dev)
 
-    # Launches of the prefill kernel (2048 workgroups) are counted in launch
-    # order, so a kernel trace of this run can pick out the timed ones.
+    # Launches of the prefill kernel are counted in launch order, so a kernel
+    # trace of this run can pick out the timed ones. At head_dim 64 with an
+    # even group size it is the head-pair kernel: one workgroup per 128-row
+    # query tile and pair of query heads.
+    prefill_wg = ((case.q.shape[2] + 127) // 128) * case.q.shape[0] * case.q.shape[1] // 2
     launches = [0]
 
     def headline(i=0):
@@ -641,13 +644,13 @@ def main():
     n_roof = max(20, args.steps)
     kern_ms = event_time_ms(roof, n_roof, 3, mark=lambda: launches[0])
     print("[bench-launches] " + json.dumps({
-        "kernel": "flash_fwd_kernel<0, 64>", "workgroups": 2048, "workload": "prefill_s2048",
+        "kernel": "cie::flash_fwd_r64_kernel<0, 64, true>", "workgroups": prefill_wg, "workload": "prefill_s2048",
         "headline_steps": [first_timed, args.steps],
         "roofline_trials": [[m, n_roof] for m in event_time_ms.marks]}), file=sys.stderr, flush=True)
     achieved = case.flops / (kern_ms / 1e3) / 1e12
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": traffic_from_summary(),
-            "kernel": "flash_fwd_kernel<fp16, D=64>", "kernel_us": round(kern_ms * 1e3, 2)}
+            "kernel": "flash_fwd_r64_kernel<fp16, D=64, head pairs>", "kernel_us": round(kern_ms * 1e3, 2)}
 
     extra = {}
     if not args.no_extra:

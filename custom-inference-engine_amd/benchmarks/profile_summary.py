@@ -34,8 +34,9 @@ import sys
 XCDS = 8            # accelerator complex dies of one MI355X; GRBM_GUI_ACTIVE is summed over them
 SIMDS = 256 * 4     # 256 CUs x 4 SIMDs; SQ_VALU_MFMA_BUSY_CYCLES is summed over them
 COPY_BYTES = 256 << 20
-PROBE_WORKLOADS = {2048: "prefill_s2048", 4096: "prefill_s16384"}
-PREFILL_KERNELS = ("cie::flash_fwd_kernel", "cie::flash_fwd_il_kernel")  # head_dim 128 runs the second
+PROBE_WORKLOADS = {1024: "prefill_s2048", 4096: "prefill_s16384"}  # by workgroup count
+# head_dim 64 runs the head-pair kernel (prefill_s2048), head_dim 128 the interleaved one
+PREFILL_KERNELS = ("cie::flash_fwd_kernel", "cie::flash_fwd_r64_kernel", "cie::flash_fwd_il_kernel")
 
 
 def _grid(r: dict) -> tuple[int, int]:
@@ -79,11 +80,10 @@ def trace(trace_csv: str, bench_stdout: str, bench_stderr: str) -> None:
     for (name, wg, thr), v in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:20]:
         print(f"| `{name[:100]}` | {wg} x {thr} | {len(v)} | {_stats(v)} | {100 * sum(v) / total:.2f} |")
 
-    kern = [r for r in rows if _name(r).startswith("cie::flash_fwd_kernel<0, 64>")
-            and _grid(r)[0] == marks["workgroups"]]
+    kern = [r for r in rows if _name(r) == marks["kernel"] and _grid(r)[0] == marks["workgroups"]]
     a, k = marks["headline_steps"]
     head = kern[a:a + k]
-    print(f"\nLaunches of `cie::flash_fwd_kernel<0, 64>` with {marks['workgroups']} workgroups "
+    print(f"\nLaunches of `{marks['kernel']}` with {marks['workgroups']} workgroups "
           f"({marks['workload']}), numbered in launch order: {len(kern)} in the run.\n")
     print("| region (launch numbers from bench.py) | launches | avg us | median us | min us | max us |")
     print("|---|---:|---:|---:|---:|---:|")

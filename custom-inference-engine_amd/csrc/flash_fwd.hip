@@ -45,6 +45,9 @@
 //
 // head_dim 128 runs flash_fwd_il_kernel below instead: same tiles and
 // softmax rules, its MFMA and VALU work issued as one interleaved stream.
+// head_dim 64 over more than 128 query rows runs flash_fwd_r64_kernel: two
+// 32-row groups per wave (the same rows of two query heads, or 64 rows of
+// one head) sharing every K/V fragment read.
 #include <type_traits>
 #include <utility>
 
@@ -463,9 +466,9 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 //    packing on the VALU) as one stream, MFMA and VALU work alternating in a
 //    fixed ratio, so the VALU work of one wave overlaps the MFMAs of both
 //    waves of its SIMD;
-//  * the row sums of the rounded probabilities come from 16x16x32 MFMAs
-//    against a 0/1 pattern (no DOT instruction: those wait for the matrix
-//    pipe), already summed over both lanes of a row.
+//  * the row sums of the rounded probabilities come from 4x4x4 MFMAs with
+//    A all ones (no DOT instruction: those wait for the matrix pipe), each
+//    lane's own values only, then one cross-lane add for the row.
 // The slow path of the lazy max acts on the rows that triggered it only, so
 // a row's arithmetic does not depend on the other rows of its wave.
 // P.V one tile behind keeps V(t-1) resident one step longer: the ring holds
@@ -841,15 +844,416 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Two row groups per wave (head_dim 64).
+//
+// Each wave owns two groups of 32 query rows and streams 32-key tiles: every
+// K fragment read from LDS feeds the QK^T MFMAs of both groups and every V^T
+// fragment the P.V MFMAs of both, so a tile's LDS reads, copies and barrier
+// serve twice the MFMA work of flash_fwd_kernel's 32-row waves. HEADS: the
+// groups are the same 32 rows of two query heads that share the kv head
+// (128-row workgroups; a wave's causal span stays 32 rows); otherwise they
+// are rows q0w + 32 rg + l32 of one head (256-row workgroups). Per tile and
+// wave: 2 -m blocks + 8 QK^T MFMAs, 32 exp2 per lane, 8 P.V MFMAs. The
+// copies, causal rule and lazy max are those of flash_fwd_kernel; the slow
+// path acts on the rows that triggered it only (as in flash_fwd_il_kernel).
+template <int D, bool HEADS>
+struct R64Cfg {
+  static constexpr int RW = HEADS ? 32 : 64;   // query rows per wave
+  static constexpr int BM = 4 * RW;            // query rows per workgroup
+  static constexpr int NRG = 2;                // 32-row groups per wave
+  static constexpr int BN = 32;                // keys per tile
+  static constexpr int S = D / 8;              // 16-byte chunks per row
+  static constexpr int DT = D / 32;            // 32-row output tiles
+  static constexpr int KK = D / 16;            // MFMA steps over head_dim
+  static constexpr int TILE = BN * D;
+  static constexpr int STAGE = 2 * TILE;       // K tile, then V tile
+  static constexpr int NST = 4;                // ring stages (measured against 6 and 8: 2 % faster)
+  static constexpr int NW = BN * S / 256;      // 1 KiB copies per wave per tensor
+  static constexpr int PER_TILE = 2 * NW;
+  static constexpr int NQK = KK * NRG;         // QK^T MFMAs per tile (plus the -m blocks)
+  static constexpr int EPC = 16 * NRG / NQK;   // S(t) elements per QK MFMA
+  static_assert(D == 64, "two row groups per wave fit the registers at head_dim 64");
+  static_assert(NW * 256 == BN * S, "tile must split evenly over 4 waves");
+  static_assert(EPC * NQK == 16 * NRG, "softmax chunks must split evenly");
+};
+
+
+template <int DTYPE, int D, bool HEADS>
+__global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams p) {
+  using C = R64Cfg<D, HEADS>;
+  using E = Elt<DTYPE>;
+  constexpr int BN = C::BN, NRG = C::NRG;
+  __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
+
+  // p.n_mt counts BM-row query tiles here and a work item is one query
+  // tile of one head (of a pair of heads with HEADS; see launch_flash_t).
+  // Each XCD takes a contiguous run of items (whole kv heads when the run
+  // divides evenly) and dispatches it longest first across all of its kv
+  // heads: items are few and long here, and kv-head-major order left long
+  // items for the end of the run.
+  const int N = p.n_wg;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int x0 = xcd * (N >> 3) + min(xcd, N & 7);           // first item of the run
+  const int cnt = (N >> 3) + (xcd < (N & 7) ? 1 : 0);         // items of the run (slot < cnt)
+  const int G = p.group, GI = HEADS ? G / 2 : G;
+  const int per_grp = p.n_mt * GI;                            // items per kv head
+  int grp, mt, g;
+  if (x0 % per_grp == 0 && cnt % per_grp == 0) {
+    const int width = (cnt / per_grp) * GI;                   // items per query tile in the run
+    const int rank = slot / width, r2 = slot - rank * width;
+    grp = x0 / per_grp + r2 / GI;
+    g = r2 - (r2 / GI) * GI;
+    mt = p.n_mt - 1 - rank;
+  } else {
+    const int logical = x0 + slot;
+    grp = logical / per_grp;
+    const int rem = logical - grp * per_grp;
+    mt = p.n_mt - 1 - rem / GI;
+    g = rem - (rem / GI) * GI;
+  }
+  const int b = grp / p.Hk, kvh = grp - b * p.Hk;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int q0w = mt * C::BM + wave * C::RW;  // first row of this wave
+  int qi[NRG], hq[NRG];                        // rows and heads owned by this lane
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg) {
+    qi[rg] = q0w + (HEADS ? 0 : 32 * rg) + l32;
+    hq[rg] = HEADS ? kvh * G + 2 * g + rg : kvh * G + g;
+  }
+
+  u32x4 qf[NRG][C::KK];
+  {
+    const float c = p.scale_log2;
+    const float cq = p.q_sign ? -c : c;
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      const uint16_t* qrow = p.q + b * p.qs0 + hq[rg] * p.qs1 + (int64_t)qi[rg] * p.qs2;
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk) qf[rg][kk] = load16(qrow + 16 * kk + 8 * hl, qi[rg] < p.Lq);
+      if (p.rope.cos)
+        rope_q_lane<DTYPE, D>(qf[rg], p.rope, (p.q_pos0 ? p.q_pos0[b] : 0) + qi[rg], qi[rg] < p.Lq, hl);
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const f32x2 v = unpack2<DTYPE>(qf[rg][kk][w]);
+          qf[rg][kk][w] = E::pack2(v[0] * cq, v[1] * cq);
+        }
+    }
+  }
+
+  const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;
+  int kend = p.Lk;
+  if (p.causal) kend = max(0, min(p.Lk, p.Lk - p.Lq + wg_last_row + 1));
+  int wave_kend = 0;
+  if (q0w < p.Lq) {
+    wave_kend = p.Lk;
+    if (p.causal) wave_kend = max(0, min(p.Lk, p.Lk - p.Lq + min(q0w + C::RW - 1, p.Lq - 1) + 1));
+  }
+  int lim[NRG];
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg) lim[rg] = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + qi[rg]) : p.Lk - 1;
+  const int wave_lim0 = p.causal ? min(p.Lk - 1, p.Lk - p.Lq + q0w) : p.Lk - 1;  // smallest lim in the wave
+  const int n_tiles = (kend + BN - 1) / BN;
+
+  const uint16_t* kb = p.k + b * p.ks0 + kvh * p.ks1;
+  const uint16_t* vb = p.v + b * p.vs0 + kvh * p.vs1;
+  const int last_key = max(p.Lk - 1, 0);
+
+  // Tile copy: as in flash_fwd_kernel (one 16-byte chunk per lane and tensor).
+  int lrow[C::NW], lchk[C::NW];
+#pragma unroll
+  for (int j = 0; j < C::NW; ++j) {
+    const int P = (wave * C::NW + j) * 64 + lane;
+    lrow[j] = P / C::S;
+    lchk[j] = 8 * ((P % C::S) ^ chunk_swizzle<C::S>(lrow[j]));
+  }
+  const bool off32 = (int64_t)BN * max(p.ks2, p.vs2) * 2 + 2 * D < ((int64_t)1 << 31);
+  uint32_t koff[C::NW], voff[C::NW];
+#pragma unroll
+  for (int j = 0; j < C::NW; ++j) {
+    koff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.ks2 + lchk[j])) : 0u;
+    voff[j] = off32 ? (uint32_t)(2 * ((int64_t)lrow[j] * p.vs2 + lchk[j])) : 0u;
+  }
+  const uint32_t ring_lds = lds_addr_of(ring);
+  auto issue = [&](int t) CIE_INLINE {
+    const int n0 = t * BN;
+    const uint32_t st = ring_lds + 2u * (uint32_t)((t % C::NST) * C::STAGE + wave * C::NW * 512);
+    if (off32 && n0 + BN <= p.Lk) {
+      const void* kt = uniform_ptr(kb + (int64_t)n0 * p.ks2);
+      const void* vt = uniform_ptr(vb + (int64_t)n0 * p.vs2);
+#pragma unroll
+      for (int j = 0; j < C::NW; ++j) {
+        dma16_sv(kt, koff[j], st + 1024u * j);
+        dma16_sv(vt, voff[j], st + 2u * C::TILE + 1024u * j);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::NW; ++j) {
+        const int key = min(n0 + lrow[j], last_key);
+        dma16_at(kb + (int64_t)key * p.ks2 + lchk[j], st + 1024u * j);
+        dma16_at(vb + (int64_t)key * p.vs2 + lchk[j], st + 2u * C::TILE + 1024u * j);
+      }
+    }
+  };
+
+  // K fragment (head_dim step kk) of the tile in stage ks: key l32 of the tile.
+  auto kfrag = [&](const uint16_t* ks, int kk) CIE_INLINE {
+    const int sl = (2 * kk + hl) ^ chunk_swizzle<C::S>(l32);
+    return *reinterpret_cast<const u32x4*>(ks + (l32 * C::S + sl) * 8);
+  };
+  // S^T of both row groups from the tile in stage ks (no -m block).
+  auto qk = [&](const uint16_t* ks, f32x16* s) CIE_INLINE {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) s[rg] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) {
+      const u32x4 a = kfrag(ks, kk);
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) s[rg] = E::mfma(a, qf[rg][kk], s[rg]);
+    }
+  };
+  // Element e of a row group's scores in a lane is key n0 + 4 hl + 8 (e / 4)
+  // + e % 4 of row qi[rg].
+  auto mask = [&](int t, f32x16* s) CIE_INLINE {
+    const int n0 = t * BN;
+    if (n0 + BN - 1 > wave_lim0) {
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+        const int r = lim[rg] - n0 - 4 * hl;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[rg][e] = 8 * (e >> 2) + (e & 3) <= r ? s[rg][e] : -INFINITY;
+      }
+    }
+  };
+  // V^T fragment (output tile dt, 16-key block cc) of the tile in stage vs.
+  const int rq = lane & 15, gq = lane >> 4;
+  auto vfrag = [&](const uint16_t* vs, int dt, int cc) CIE_INLINE {
+    const int d = 32 * dt + 16 * (gq & 1) + 4 * (rq & 3);
+    const int chunk = d >> 3, within = d & 7;
+    const int tlo = 16 * cc + 4 * hl + (rq >> 2);
+    const int thi = tlo + 8;
+    const u32x2 lo = lds_read_tr16(vs + (tlo * C::S + (chunk ^ chunk_swizzle<C::S>(tlo))) * 8 + within);
+    const u32x2 hi = lds_read_tr16(vs + (thi * C::S + (chunk ^ chunk_swizzle<C::S>(thi))) * 8 + within);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+
+  f32x16 acc[NRG][C::DT];
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) acc[rg][dt] = f32x16{};
+  float m[NRG], l[NRG];  // l: the row's sum over both lanes
+  uint32_t bm[NRG];      // word 0 of the -m block's B operand
+  constexpr float kMScale = DTYPE == 0 ? 256.f : 1.f;  // fp16 range for |m| up to 2^24
+  const u32x4 a_one = {hl == 0 ? E::pack2(kMScale, 0.f) : 0u, 0u, 0u, 0u};
+  auto set_m = [&](int rg, float x) CIE_INLINE {  // m = x rounded to what the B operand holds exactly
+    if (x != -INFINITY) {
+      x = fminf(x, 65504.f * kMScale);
+      x = unpack2<DTYPE>(E::pack2(x * (1.f / kMScale), 0.f))[0] * kMScale;
+    }
+    m[rg] = x;
+    bm[rg] = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
+  };
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg) {
+    m[rg] = -INFINITY;
+    l[rg] = 0.f;
+    bm[rg] = 0u;
+  }
+  // Row sums of P: 4x4x4 MFMAs with A all ones (see flash_fwd_kernel).
+  const u32x2 sum_ones = {E::pack2(1.f, 1.f), E::pack2(1.f, 1.f)};
+
+  vm_wait<0>();  // q (and RoPE tables) in registers before the copies start
+  const int pro = min(C::NST - 1, n_tiles);
+  for (int t = 0; t < pro; ++t) issue(t);
+
+  f32x16 sc[NRG];
+  if (n_tiles > 0) {
+    wait_tiles<C::PER_TILE, 2>(pro - 1);
+    __syncthreads();
+    qk(ring, sc);
+    mask(0, sc);
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      set_m(rg, xhalf_max(max16(sc[rg])));  // the reference max starts at tile 0's row max
+      sc[rg] -= m[rg] == -INFINITY ? 0.f : m[rg];
+    }
+  }
+
+  // One pipeline step: sc holds S(t) - m, S(t+1) - m is produced in sn; ST is
+  // the ring stage of tile t.
+  auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
+    constexpr int st = decltype(ST)::value, st1 = (st + 1) % C::NST;
+    if (t + 1 < n_tiles) {
+      wait_tiles<C::PER_TILE, 2>(min(C::NST - 3, n_tiles - 2 - t));
+      __syncthreads();  // tile t+1 resident for all waves; stage of tile t-1 free
+      if (t + C::NST - 1 < n_tiles) issue(t + C::NST - 1);
+    }
+    if (t * BN >= wave_kend) return;  // wave-uniform: every row of the wave is done
+
+    // S(t+1) on the MFMA pipe, P(t) on the VALU (as in flash_fwd_kernel).
+    __builtin_amdgcn_s_setprio(1);
+    u32x4 pb[NRG][2];                 // P(t): row group, 16-key block
+    f32x4 tsm[NRG];                   // this lane's sums of the tile's p
+    {
+      const uint16_t* ks = ring + st1 * C::STAGE;
+      u32x4 ka[C::KK];
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk) ka[kk] = kfrag(ks, kk);
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+        sn[rg] = E::mfma(a_one, u32x4{bm[rg], 0u, 0u, 0u}, f32x16{});
+        tsm[rg] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int i = 0; i < C::NQK; ++i) {
+        const int kk = i / NRG, rgq = i % NRG;
+        sn[rgq] = E::mfma(ka[kk], qf[rgq][kk], sn[rgq]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = i * C::EPC; e < (i + 1) * C::EPC; ++e) {
+          const int rg = e / 16, ee = e % 16;
+          sc[rg][ee] = exp2_fast(sc[rg][ee]);
+          if (ee & 1) {
+            const uint32_t pk = E::pack2(sc[rg][ee - 1], sc[rg][ee]);
+            asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
+            pb[rg][ee >> 3][(ee & 7) >> 1] = pk;
+          }
+          if ((ee & 3) == 3) {
+            const int c = ee >> 3, w = (ee & 7) >> 1;
+            tsm[rg] = E::mfma4(sum_ones, u32x2{pb[rg][c][w - 1], pb[rg][c][w]}, tsm[rg]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+
+    // Lazy-max check: a row whose tile sum of p passed 2^10 recomputes S(t)
+    // from the resident K tile, raises m to its row max, rescales O and l and
+    // redoes its p; the other rows keep theirs.
+    float ts[NRG];
+    bool trig[NRG];
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      ts[rg] = xhalf_sum(tsm[rg][0]);
+      trig[rg] = !(ts[rg] <= kSumTrigger);
+    }
+    if (__builtin_amdgcn_ballot_w64(trig[0] || trig[1])) {
+      qk(ring + st * C::STAGE, sc);
+      mask(t, sc);
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+        const float mx = xhalf_max(max16(sc[rg]));
+        const float m_old = m[rg];
+        if (trig[rg]) set_m(rg, maxf(m_old, mx));
+        const float alpha = m[rg] > m_old ? exp2_fast(m_old - m[rg]) : 1.f;  // 0 when m was -inf
+        l[rg] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) acc[rg][dt] *= alpha;
+        const float nm = m[rg] == -INFINITY ? 0.f : -m[rg];
+        const float adj = (m_old == -INFINITY ? 0.f : m_old) + nm;  // 0 for rows that keep m
+        sn[rg] += adj;
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const uint32_t w = pb[rg][e >> 3][(e & 7) >> 1];
+          pb[rg][e >> 3][(e & 7) >> 1] =
+              trig[rg] ? E::pack2(exp2_fast(sc[rg][e] + nm), exp2_fast(sc[rg][e + 1] + nm)) : w;
+        }
+        f32x4 t2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          t2 = E::mfma4(sum_ones, u32x2{pb[rg][cc][0], pb[rg][cc][1]}, t2);
+          t2 = E::mfma4(sum_ones, u32x2{pb[rg][cc][2], pb[rg][cc][3]}, t2);
+        }
+        const float ts2 = xhalf_sum(t2[0]);
+        if (trig[rg]) ts[rg] = ts2;
+      }
+    }
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) l[rg] += ts[rg];
+    mask(t + 1, sn);
+
+    // O += V(t) P(t): each V^T fragment serves both row groups.
+    {
+      const uint16_t* vs = ring + st * C::STAGE + C::TILE;
+      u32x4 va[C::DT][2];
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) va[dt][cc] = vfrag(vs, dt, cc);
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+          for (int dt = 0; dt < C::DT; ++dt) acc[rg][dt] = E::mfma(va[dt][cc], pb[rg][cc], acc[rg][dt]);
+    }
+  };
+  f32x16 sb[NRG];
+  static_assert(C::NST % 2 == 0, "stage and score buffer repeat after NST steps");
+  for (int t = 0; t < n_tiles; t += C::NST) {
+    static_for<C::NST>([&](auto I) CIE_INLINE {
+      constexpr int i = decltype(I)::value;
+      if (t + i < n_tiles) {
+        if constexpr (i % 2 == 0) step(std::integral_constant<int, i>{}, t + i, sc, sb);
+        else step(std::integral_constant<int, i>{}, t + i, sb, sc);
+      }
+    });
+  }
+
+  // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
+  // reference's softmax over an all -inf row; Lk == 0 gives zeros.
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg) {
+    const float inv = p.Lk == 0 ? 0.f : 1.f / l[rg];
+    if (qi[rg] < p.Lq) {
+      uint16_t* orow = p.o + b * p.os0 + hq[rg] * p.os1 + (int64_t)qi[rg] * p.os2;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = 32 * dt + 8 * g4 + 4 * hl;
+          const u32x2 w = {E::pack2(acc[rg][dt][4 * g4] * inv, acc[rg][dt][4 * g4 + 1] * inv),
+                           E::pack2(acc[rg][dt][4 * g4 + 2] * inv, acc[rg][dt][4 * g4 + 3] * inv)};
+          *reinterpret_cast<u32x2*>(orow + d) = w;
+        }
+      }
+    }
+  }
+}
+
 // head_dim 128 runs the interleaved kernel (S=16384 bf16 causal: 1863 ->
 // 1774 us); at head_dim 64 it measured 2 % slower than flash_fwd_kernel, whose
 // VALU-heavy and MFMA-only phases the other wave of each SIMD pairs up.
+// head_dim 64 over more than 128 query rows runs the two-row-group kernel:
+// on pairs of query heads when the group size is even, else on 256-row query
+// tiles (both modes give every row the same arithmetic, so GQA equals its
+// expanded MHA bit for bit). One query tile (prefill_s128: 5.8 against 7.5 us
+// as head pairs) stays on flash_fwd_kernel's more, shorter workgroups.
+template <int DTYPE, int D, bool HEADS>
+static void launch_r64(const FlashParams& p, hipStream_t stream) {
+  FlashParams q = p;
+  q.n_mt = (p.Lq + R64Cfg<D, HEADS>::BM - 1) / R64Cfg<D, HEADS>::BM;
+  q.n_wg = q.n_mt * (p.n_wg / p.n_mt) / (HEADS ? 2 : 1);  // B * Hq (/ 2) items per query tile
+  hipLaunchKernelGGL((flash_fwd_r64_kernel<DTYPE, D, HEADS>), dim3(q.n_wg), dim3(256), 0, stream, q);
+}
+
 template <int DTYPE, int D>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t stream) {
-  if constexpr (D == 128)
+  if constexpr (D == 128) {
     hipLaunchKernelGGL((flash_fwd_il_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
-  else
+  } else if constexpr (D == 64) {
+    if (p.Lq <= 128) hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+    else if (p.group % 2 == 0) launch_r64<DTYPE, D, true>(p, stream);
+    else launch_r64<DTYPE, D, false>(p, stream);
+  } else {
     hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -32,7 +32,7 @@ struct FlashParams {
   int64_t vs0, vs1, vs2;
   int64_t os0, os1, os2;
   int B, Hq, Hk, Lq, Lk, group;
-  int n_mt;  // query tiles of 128 rows
+  int n_mt;  // query tiles of 128 rows (the launcher recounts them for kernels with other tiles)
   int n_wg;  // B * Hq * n_mt
   float scale_log2;  // |scale| * log2(e), never below 1e-30
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative

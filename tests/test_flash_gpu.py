@@ -88,6 +88,25 @@ def test_d128_every_tile_count(L, dtype, causal):
     assert_close(out, ref, TOL[dtype], f"D=128 L={L} {dtype} causal={causal}")
 
 
+@pytest.mark.parametrize("Lq,Lk", [(129, 129), (160, 160), (191, 191), (192, 192), (255, 255), (256, 256),
+                                   (257, 257), (300, 311), (383, 383), (384, 384), (385, 385), (511, 511),
+                                   (512, 512), (513, 513), (200, 1000), (520, 70)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("H,Hk", [(4, 2), (3, 3)])
+def test_d64_two_row_group_kernel(Lq, Lk, dtype, causal, H, Hk):
+    """D=64 with more than 128 query rows runs two 32-row groups per wave over
+    32-key tiles in a four-stage ring: the same rows of two query heads (even
+    group size, 128-row workgroups) or 64 rows of one head (odd group size,
+    256-row workgroups). 1..33 tiles, full and ragged query and key tails,
+    waves with no rows, a history longer than the chunk and more queries than
+    keys (NaN rows under the causal rule)."""
+    q, k, v = _inputs(1, H, Hk, Lq, Lk, 64, dtype, seed=2000 + Lq + Lk, vscale=0.5)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=causal)
+    assert_close(out, ref, TOL[dtype], f"D=64 Lq={Lq} Lk={Lk} {dtype} causal={causal}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_more_queries_than_keys_gives_nan_rows(dtype):
     q, k, v = _inputs(1, 4, 2, 150, 20, 64, dtype, seed=5, vscale=0.5)
@@ -124,42 +143,49 @@ def test_strided_views_match_contiguous():
     assert torch.equal(out, out_c)
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_gqa_equals_expanded_mha_bitwise(D):
-    q, k, v = _inputs(2, 8, 2, 100, 140, D, torch.float16, seed=9)
+@pytest.mark.parametrize("D,Lq,Lk", [(64, 100, 140), (64, 300, 340), (128, 100, 140)])
+def test_gqa_equals_expanded_mha_bitwise(D, Lq, Lk):
+    """GQA indexes the shared kv head instead of copying it; at D=64 over more
+    than 128 rows it also runs head pairs where the expanded MHA (group size
+    1) runs 64-row waves of one head, and both give every row the same bits."""
+    q, k, v = _inputs(2, 8, 2, Lq, Lk, D, torch.float16, seed=9)
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
     gqa = flash_attention(q, k, v, causal=True)
     mha = flash_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), causal=True)
     assert torch.equal(gqa, mha)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D,L", [(64, 96), (64, 300), (128, 96)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_nan_query_row_stays_in_its_row(D, dtype):
+def test_nan_query_row_stays_in_its_row(D, L, dtype):
     """A NaN in one query row makes that row NaN and no other, as the
     reference's per-row softmax does (the row sums run on the matrix pipe
     and must not mix rows: rows r and r + 16 of a wave once shared an MFMA
     column, where 0 x NaN = NaN)."""
-    q, k, v = _inputs(1, 4, 2, 96, 96, D, dtype, seed=23)
+    q, k, v = _inputs(1, 4, 2, L, L, D, dtype, seed=23)
     qn = q.clone()
     qn[0, 1, 0, 3] = float("nan")
     qn[0, 2, 37, 0] = float("nan")
+    if L > 128:  # the second row group of a 64-row wave
+        qn[0, 3, 64 + 33, 5] = float("nan")
     clean = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
     out = flash_attention(qn.to(DEV), k.to(DEV), v.to(DEV), causal=True)
     ref = flash_attention_ref(qn.float(), k.float(), v.float(), causal=True)
-    assert_close(out, ref, TOL[dtype], f"nan rows D={D} {dtype}")  # includes the NaN pattern
-    if D == 128:  # the slow path there acts per row: the other rows keep their bits
+    assert_close(out, ref, TOL[dtype], f"nan rows D={D} L={L} {dtype}")  # includes the NaN pattern
+    if D == 128 or L > 128:  # the slow path there acts per row: the other rows keep their bits
         keep = ~torch.isnan(ref).any(dim=-1)
         assert torch.equal(out.cpu()[keep], clean.cpu()[keep])
 
 
+@pytest.mark.parametrize("D,span", [(128, 32), (64, 64)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_d128_rows_do_not_depend_on_their_wave(dtype):
-    """head_dim 128: a row whose scores rise across tiles takes the lazy-max
-    slow path; the other rows of its wave (rows 1..31 of the same 32-row
-    strip) keep their arithmetic, so their outputs are bit-identical to a run
-    in which no row of the strip takes it."""
-    D, L = 128, 320
+def test_rows_do_not_depend_on_their_wave(D, span, dtype):
+    """head_dim 128 (32-row waves) and head_dim 64 over more than 128 query
+    rows (waves of 32 rows of both query heads here): a row whose scores rise
+    across tiles takes the lazy-max slow path; the other rows (1..span-1 of
+    both heads, its own wave included) keep their arithmetic, so their
+    outputs are bit-identical to a run in which no row takes it."""
+    L = 320
     g = torch.Generator().manual_seed(21)
     u = torch.randn(D, generator=g)
     u = u / u.norm()
@@ -172,7 +198,7 @@ def test_d128_rows_do_not_depend_on_their_wave(dtype):
     loud[:, :, 0] += 3.0 * u  # row 0 (and its wave's slow path) rises with the keys
     outs = [flash_attention(x.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=False)
             for x in (quiet, loud)]
-    assert torch.equal(outs[0][:, :, 1:32], outs[1][:, :, 1:32])
+    assert torch.equal(outs[0][:, :, 1:span], outs[1][:, :, 1:span])
     ref = flash_attention_ref(loud.to(dtype).float(), k.to(dtype).float(), v.to(dtype).float(), causal=False)
     assert_close(outs[1], ref, TOL[dtype], f"loud row {dtype}")
 
