@@ -72,17 +72,25 @@ constexpr int kI8MaxSplitTiles = 256;  // K is split only when there are fewer (
 
 constexpr int kI8MaxSplits = 16;
 
-template <int MT, int NST_>
+// KW: waves per 32 weight rows. With KW = 2 (eight waves) waves w and w + 4
+// take the two 32-k halves of every step for the same weight rows and are
+// summed through LDS at the end, so one workgroup per CU still puts two
+// waves on every SIMD.
+template <int MT, int NST_, int KW = 1>
 struct I8Cfg {
   static constexpr int BM = 32 * MT;
   static constexpr int NST = NST_;  // LDS ring stages
+  static constexpr int NT = 256 * KW;                    // threads
   static constexpr int X_BYTES = BM * kI8BK * 2;        // x tile per stage
   static constexpr int W_BYTES = kI8BN * kI8BK;         // w tile per stage
   static constexpr int STAGE = X_BYTES + W_BYTES;
-  static constexpr int XI = X_BYTES / (256 * 16);       // x copies per lane per stage
-  static constexpr int WI = W_BYTES / (256 * 16);       // w copies per lane per stage
+  static constexpr int XI = X_BYTES / (NT * 16);        // x copies per lane per stage
+  static constexpr int WI = W_BYTES / (NT * 16);        // w copies per lane per stage
   static constexpr int PER = XI + WI;
-  static_assert(XI >= 1 && WI == 2, "tile must split over 4 waves");
+  static constexpr int G2 = 2 / KW;                     // 32-k halves of a step per wave
+  static_assert(KW == 1 || KW == 2, "one or two waves per 32 weight rows");
+  static_assert(XI >= 1 && WI * KW == 2, "tile must split over the waves");
+  static_assert(NST * STAGE >= 4 * MT * 16 * 64 * 4, "the k-half partials fit the ring");
   static_assert(PER * (NST - 1) < 64, "vmcnt range");
 };
 
@@ -186,9 +194,9 @@ __device__ __forceinline__ void wait_steps_ahead(int ahead) {
   }
 }
 
-template <int DTYPE, int MT, int NST>
-__global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p) {
-  using C = I8Cfg<MT, NST>;
+template <int DTYPE, int MT, int NST, int KW>
+__global__ __launch_bounds__(256 * KW, KW == 1 ? 2 : 1) void int8_gemm_kernel(const I8GemmParams p) {
+  using C = I8Cfg<MT, NST, KW>;
   using E = Elt<DTYPE>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
@@ -208,7 +216,8 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
   const int T = ks1 - ks0;
 
   const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave 0 .. 4 KW - 1
+  const int w = wv & 3, kh = KW == 1 ? 0 : wv >> 2;  // 32 weight rows w, k half kh
   const int r32 = lane & 31, hk = lane >> 5;
   const uint32_t lds0 = lds_addr_of(smem);
 
@@ -218,21 +227,21 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
   uint32_t xdst[C::XI];
 #pragma unroll
   for (int j = 0; j < C::XI; ++j) {
-    const int P = (j * 4 + w) * 64 + lane;  // x chunk slot in the tile: 8 per row
+    const int P = (j * 4 * KW + wv) * 64 + lane;  // x chunk slot in the tile: 8 per row
     const int r = P >> 3, c = (P & 7) ^ chunk_swizzle<8>(r);
     const int m = min(m0 + r, p.M - 1);
     xsrc[j] = reinterpret_cast<const uint8_t*>(p.x + (int64_t)m * p.xs + 8 * c);
-    xdst[j] = (uint32_t)((j * 4 + w) * 64 * 16);
+    xdst[j] = (uint32_t)((j * 4 * KW + wv) * 64 * 16);
   }
   const uint8_t* wsrc[C::WI];
   uint32_t wdst[C::WI];
 #pragma unroll
   for (int j = 0; j < C::WI; ++j) {
-    const int P = (j * 4 + w) * 64 + lane;  // w chunk slot: 4 per row
+    const int P = (j * 4 * KW + wv) * 64 + lane;  // w chunk slot: 4 per row
     const int r = P >> 2, c = (P & 3) ^ chunk_swizzle<4>(r);
     const int n = min(n0 + r, p.N - 1);
     wsrc[j] = reinterpret_cast<const uint8_t*>(p.w) + (int64_t)n * p.wsr + 16 * c;
-    wdst[j] = (uint32_t)(C::X_BYTES + (j * 4 + w) * 64 * 16);
+    wdst[j] = (uint32_t)(C::X_BYTES + (j * 4 * KW + wv) * 64 * 16);
   }
   auto issue = [&](int t) {
     const uint32_t st = lds0 + (uint32_t)((t % C::NST) * C::STAGE);
@@ -244,19 +253,24 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
     for (int j = 0; j < C::WI; ++j) dma16_at(wsrc[j] + kw, st + wdst[j]);
   };
 
-  // fragment read offsets within a stage (bytes)
-  uint32_t woff[2], xoff[MT][2][2];
+  // fragment read offsets within a stage (bytes), for this wave's k halves
+  // g2 = kh G2 + i of each step
+  uint32_t woff[C::G2], xoff[MT][C::G2][2];
   {
     const int r = w * 32 + r32;
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2) woff[g2] = C::X_BYTES + r * 64 + 16 * ((2 * g2 + hk) ^ chunk_swizzle<4>(r));
+    for (int i = 0; i < C::G2; ++i) {
+      const int g2 = kh * C::G2 + i;
+      woff[i] = C::X_BYTES + r * 64 + 16 * ((2 * g2 + hk) ^ chunk_swizzle<4>(r));
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int rx = mt * 32 + r32;
 #pragma unroll
-      for (int g2 = 0; g2 < 2; ++g2)
+      for (int i = 0; i < C::G2; ++i)
 #pragma unroll
-        for (int g = 0; g < 2; ++g) xoff[mt][g2][g] = rx * 128 + 16 * ((4 * g2 + 2 * hk + g) ^ chunk_swizzle<8>(rx));
+        for (int g = 0; g < 2; ++g)
+          xoff[mt][i][g] = rx * 128 + 16 * ((4 * (kh * C::G2 + i) + 2 * hk + g) ^ chunk_swizzle<8>(rx));
     }
   }
 
@@ -276,26 +290,45 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const I8GemmParams p)
     const uint8_t* st = smem + (t % C::NST) * C::STAGE;
     // every fragment of the step is read first, so the LDS latency is paid
     // once per step rather than in front of each MFMA
-    u32x4 wq[2], xb[MT][2][2];
+    // (this wave's k halves g2 = kh G2 .. kh G2 + G2 - 1 of the step)
+    u32x4 wq[C::G2], xb[MT][C::G2][2];
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2) wq[g2] = *reinterpret_cast<const u32x4*>(st + woff[g2]);
+    for (int i = 0; i < C::G2; ++i) wq[i] = *reinterpret_cast<const u32x4*>(st + woff[i]);
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2)
+    for (int i = 0; i < C::G2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int g = 0; g < 2; ++g) xb[mt][g2][g] = *reinterpret_cast<const u32x4*>(st + xoff[mt][g2][g]);
+        for (int g = 0; g < 2; ++g) xb[mt][i][g] = *reinterpret_cast<const u32x4*>(st + xoff[mt][i][g]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2) {
+    for (int i = 0; i < C::G2; ++i) {
       u32x4 a0, a1;
-      dequant16<DTYPE>(wq[g2], a0, a1);
+      dequant16<DTYPE>(wq[i], a0, a1);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        acc[mt] = E::mfma(a0, xb[mt][g2][0], acc[mt]);
-        acc[mt] = E::mfma(a1, xb[mt][g2][1], acc[mt]);
+        acc[mt] = E::mfma(a0, xb[mt][i][0], acc[mt]);
+        acc[mt] = E::mfma(a1, xb[mt][i][1], acc[mt]);
       }
     }
+  }
+  if constexpr (KW == 2) {
+    // the k-half-1 sums join the k-half-0 ones through LDS (fixed order:
+    // half 0 + half 1); the ring is free once every wave has left the loop
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+    if (kh == 1) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[((w * MT + mt) * 16 + e) * 64 + lane] = acc[mt][e];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[mt][e] += red[((w * MT + mt) * 16 + e) * 64 + lane];
   }
 
   // C[i][j] of a 32x32 tile: lane j + 32 * ((i / 4) % 2), element (i / 8) * 4 + i % 4;
@@ -734,10 +767,20 @@ template <int DTYPE, int MT, int NST>
 static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, hipStream_t stream) {
   using C = I8Cfg<MT, NST>;
   if (lds != (size_t)C::NST * C::STAGE) return hipErrorInvalidValue;  // geometry and kernel disagree
-  const hipError_t attr = set_dynamic_lds(reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST>), C::NST * C::STAGE);
-  if (attr != hipSuccess) return attr;
   const int nwg = p.n_tiles * p.m_tiles * p.splits;
-  hipLaunchKernelGGL((int8_gemm_kernel<DTYPE, MT, NST>), dim3(nwg), dim3(256), lds, stream, p);
+  // one workgroup per CU or fewer: eight waves (two k halves) so every SIMD
+  // holds two waves (512 x 4096 x 4096: 31.9 -> 30.1 us); else four waves and
+  // two workgroups per CU. Not with K split three ways or more (128 x 4096 x
+  // 4096, four splits: 1 % slower).
+  const bool kw2 = nwg <= kPagedCUs && p.splits <= 2;
+  const void* fn = kw2 ? reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST, 2>)
+                       : reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST, 1>);
+  const hipError_t attr = set_dynamic_lds(fn, C::NST * C::STAGE);
+  if (attr != hipSuccess) return attr;
+  if (kw2)
+    hipLaunchKernelGGL((int8_gemm_kernel<DTYPE, MT, NST, 2>), dim3(nwg), dim3(512), lds, stream, p);
+  else
+    hipLaunchKernelGGL((int8_gemm_kernel<DTYPE, MT, NST, 1>), dim3(nwg), dim3(256), lds, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int64_t slots = (int64_t)p.n_tiles * p.m_tiles * 4 * MT * 4 * 64;

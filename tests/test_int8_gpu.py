@@ -62,7 +62,10 @@ def _exact_case(M, N, K, dtype, seed, bias):
                                    (1, 32, 32), (1, 17, 8), (1, 4096, 100), (1, 300, 4100), (2, 64, 32),
                                    (3, 300, 96), (12, 520, 100), (40, 333, 4100), (64, 128, 32), (64, 96, 17),
                                    (65, 512, 4100), (512, 1024, 4100), (100, 127, 96), (300, 96, 32), (2048, 256, 100),
-                                   (130, 4096, 4132)])
+                                   (130, 4096, 4132),
+                                   # the eight-wave tiled kernel (one workgroup per CU): two K
+                                   # splits with a K tail, one split over 64 steps
+                                   (256, 4096, 1060), (512, 2048, 4096)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_exact_arithmetic_is_bit_exact(M, N, K, dtype):
     for bias in (False, True):
