@@ -45,9 +45,10 @@
 //
 // head_dim 128 runs flash_fwd_il_kernel below instead: same tiles and
 // softmax rules, its MFMA and VALU work issued as one interleaved stream.
-// head_dim 64 over more than 128 query rows runs flash_fwd_r64_kernel: two
-// 32-row groups per wave (the same rows of two query heads, or 64 rows of
-// one head) sharing every K/V fragment read.
+// head_dim 64 launches with enough work (r64_pays) run flash_fwd_r64_kernel:
+// two 32-row groups per wave (the same rows of two query heads, or 64 rows
+// of one head) sharing every K/V fragment read.
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -1230,11 +1231,39 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
 // head_dim 128 runs the interleaved kernel (S=16384 bf16 causal: 1863 ->
 // 1774 us); at head_dim 64 it measured 2 % slower than flash_fwd_kernel, whose
 // VALU-heavy and MFMA-only phases the other wave of each SIMD pairs up.
-// head_dim 64 over more than 128 query rows runs the two-row-group kernel:
-// on pairs of query heads when the group size is even, else on 256-row query
-// tiles (both modes give every row the same arithmetic, so GQA equals its
-// expanded MHA bit for bit). One query tile (prefill_s128: 5.8 against 7.5 us
-// as head pairs) stays on flash_fwd_kernel's more, shorter workgroups.
+// head_dim 64 runs the two-row-group kernel (on pairs of query heads when
+// the group size is even, else on 256-row query tiles; both modes give every
+// row the same arithmetic) when r64_pays says so, else flash_fwd_kernel.
+//
+// A two-row-group item is twice the work of a flash_fwd_kernel item and there
+// are half as many, so it pays only with enough of them: at least one per
+// workgroup slot of the GPU (256 CUs x 2), and, causal, its longest item
+// (the last query tile: every key, 32 per step, plus ~4 steps of start-up)
+// within 1.6x the average work per slot; otherwise the critical path or the
+// idle slots cost more than the shared fragment reads save (measured on
+// B x S x Hq / Hk = 1x4096x32/8 causal 101 against 78 us, 2x1024x32/8 27 against
+// 20, 1x512x32/8 16 against 10; gains on 4x2048x32/8 78 against 86, 8x512x32/8
+// 21 against 23, 16x256x32/8 16 against 18, 1x4096x32/8 non-causal 134 against
+// 143). The estimate uses B * Hq / 2 items of 128 rows whatever the group
+// size, so GQA and its expanded MHA take the same kernel and stay equal bit
+// for bit.
+static bool r64_pays(const FlashParams& p) {
+  constexpr int64_t kSlots = 2 * kPagedCUs, kStartup = 4;
+  if (p.Lq <= 128) return false;
+  const int64_t n_mt = (p.Lq + 127) / 128;
+  const int64_t items = (int64_t)(p.n_wg / p.n_mt) / 2;  // B * Hq / 2 per query tile
+  if (n_mt * items < kSlots) return false;
+  if (!p.causal) return true;
+  int64_t work = 0, longest = 0;
+  for (int64_t mt = 0; mt < n_mt; ++mt) {
+    const int64_t kend = std::max<int64_t>(0, std::min<int64_t>(p.Lk, (int64_t)p.Lk - p.Lq + std::min<int64_t>(p.Lq, 128 * (mt + 1))));
+    const int64_t steps = (kend + 31) / 32 + kStartup;
+    work += steps;
+    longest = std::max(longest, steps);
+  }
+  return longest * kSlots * 10 <= 16 * work * items;
+}
+
 template <int DTYPE, int D, bool HEADS>
 static void launch_r64(const FlashParams& p, hipStream_t stream) {
   FlashParams q = p;
@@ -1248,7 +1277,7 @@ static hipError_t launch_flash_t(const FlashParams& p, hipStream_t stream) {
   if constexpr (D == 128) {
     hipLaunchKernelGGL((flash_fwd_il_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
   } else if constexpr (D == 64) {
-    if (p.Lq <= 128) hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+    if (!r64_pays(p)) hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
     else if (p.group % 2 == 0) launch_r64<DTYPE, D, true>(p, stream);
     else launch_r64<DTYPE, D, false>(p, stream);
   } else {

@@ -34,6 +34,43 @@ def assert_close(out: torch.Tensor, ref: torch.Tensor, tol: float, what: str = "
     return err
 
 
+def two_row_group_kernel_runs(B, H, Lq, Lk, causal):
+    """Whether a head_dim-64 launch takes the two-row-group kernel: restates
+    the launcher's rule (r64_pays, csrc/flash_fwd.hip) -- at least one item of
+    B * H / 2 per 128-row query tile for each of the 512 workgroup slots and,
+    causal, the longest item (32 keys a step, plus 4) within 1.6x the
+    average work per slot."""
+    if Lq <= 128:
+        return False
+    n_mt = (Lq + 127) // 128
+    items = B * H // 2
+    if n_mt * items < 512:
+        return False
+    if not causal:
+        return True
+    work = longest = 0
+    for mt in range(n_mt):
+        kend = max(0, min(Lk, Lk - Lq + min(Lq, 128 * (mt + 1))))
+        st = (kend + 31) // 32 + 4
+        work += st
+        longest = max(longest, st)
+    return longest * 512 * 10 <= 16 * work * items
+
+
+def batch_for_two_row_groups(H, Lq, Lk, causal):
+    """The smallest batch whose launch takes the two-row-group kernel."""
+    for B in range(1, 1025):
+        if two_row_group_kernel_runs(B, H, Lq, Lk, causal):
+            return B
+    raise AssertionError("no batch size reaches the two-row-group kernel")
+
+
+def replicate(x, B):
+    """x (1, ...) repeated B times along the batch: every copy is an independent
+    item of the launch and must give the same outputs."""
+    return x.expand(B, *x.shape[1:]).contiguous()
+
+
 def _inputs(B, H, Hk, Lq, Lk, D, dtype, seed, vscale=1.0):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(B, H, Lq, D, generator=g).to(dtype)
@@ -95,16 +132,19 @@ def test_d128_every_tile_count(L, dtype, causal):
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("H,Hk", [(4, 2), (3, 3)])
 def test_d64_two_row_group_kernel(Lq, Lk, dtype, causal, H, Hk):
-    """D=64 with more than 128 query rows runs two 32-row groups per wave over
+    """D=64 launches with enough work run two 32-row groups per wave over
     32-key tiles in a four-stage ring: the same rows of two query heads (even
     group size, 128-row workgroups) or 64 rows of one head (odd group size,
-    256-row workgroups). 1..33 tiles, full and ragged query and key tails,
-    waves with no rows, a history longer than the chunk and more queries than
-    keys (NaN rows under the causal rule)."""
+    256-row workgroups). One problem is repeated over a batch large enough to
+    take that kernel and every copy is checked against the oracle: 1..33
+    tiles, full and ragged query and key tails, waves with no rows, a
+    history longer than the chunk and more queries than keys (NaN rows under
+    the causal rule)."""
     q, k, v = _inputs(1, H, Hk, Lq, Lk, 64, dtype, seed=2000 + Lq + Lk, vscale=0.5)
-    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
     ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=causal)
-    assert_close(out, ref, TOL[dtype], f"D=64 Lq={Lq} Lk={Lk} {dtype} causal={causal}")
+    B = batch_for_two_row_groups(H, Lq, Lk, causal)
+    out = flash_attention(replicate(q, B).to(DEV), replicate(k, B).to(DEV), replicate(v, B).to(DEV), causal=causal)
+    assert_close(out, replicate(ref, B), TOL[dtype], f"D=64 Lq={Lq} Lk={Lk} {dtype} causal={causal} B={B}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -143,12 +183,16 @@ def test_strided_views_match_contiguous():
     assert torch.equal(out, out_c)
 
 
-@pytest.mark.parametrize("D,Lq,Lk", [(64, 100, 140), (64, 300, 340), (128, 100, 140)])
-def test_gqa_equals_expanded_mha_bitwise(D, Lq, Lk):
-    """GQA indexes the shared kv head instead of copying it; at D=64 over more
-    than 128 rows it also runs head pairs where the expanded MHA (group size
-    1) runs 64-row waves of one head, and both give every row the same bits."""
-    q, k, v = _inputs(2, 8, 2, Lq, Lk, D, torch.float16, seed=9)
+@pytest.mark.parametrize("D,B,Lq,Lk", [(64, 2, 100, 140), (64, 2, 300, 340), (64, 64, 300, 340), (64, 32, 1024, 1024),
+                                      (128, 2, 100, 140)])
+def test_gqa_equals_expanded_mha_bitwise(D, B, Lq, Lk):
+    """GQA indexes the shared kv head instead of copying it. At D=64 with
+    enough work (B = 64 and 32 here) it runs head pairs where the expanded
+    MHA (group size 1) runs 64-row waves of one head; the launcher decides
+    from B * Hq alone, and both give every row the same bits."""
+    if D == 64 and B >= 32:
+        assert two_row_group_kernel_runs(B, 8, Lq, Lk, True)
+    q, k, v = _inputs(B, 8, 2, Lq, Lk, D, torch.float16, seed=9)
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
     gqa = flash_attention(q, k, v, causal=True)
     mha = flash_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), causal=True)
@@ -166,14 +210,16 @@ def test_nan_query_row_stays_in_its_row(D, L, dtype):
     qn = q.clone()
     qn[0, 1, 0, 3] = float("nan")
     qn[0, 2, 37, 0] = float("nan")
-    if L > 128:  # the second row group of a 64-row wave
+    if L > 128:  # the other head of a pair, and row group 1 of a 64-row wave
         qn[0, 3, 64 + 33, 5] = float("nan")
-    clean = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
-    out = flash_attention(qn.to(DEV), k.to(DEV), v.to(DEV), causal=True)
     ref = flash_attention_ref(qn.float(), k.float(), v.float(), causal=True)
-    assert_close(out, ref, TOL[dtype], f"nan rows D={D} L={L} {dtype}")  # includes the NaN pattern
+    B = batch_for_two_row_groups(4, L, L, True) if L > 128 else 1  # D=64: the two-row-group kernel
+    q, qn, k, v = (replicate(x, B).to(DEV) for x in (q, qn, k, v))
+    clean = flash_attention(q, k, v, causal=True)
+    out = flash_attention(qn, k, v, causal=True)
+    assert_close(out, replicate(ref, B), TOL[dtype], f"nan rows D={D} L={L} {dtype}")  # includes the NaN pattern
     if D == 128 or L > 128:  # the slow path there acts per row: the other rows keep their bits
-        keep = ~torch.isnan(ref).any(dim=-1)
+        keep = ~torch.isnan(replicate(ref, B)).any(dim=-1)
         assert torch.equal(out.cpu()[keep], clean.cpu()[keep])
 
 
@@ -196,11 +242,12 @@ def test_rows_do_not_depend_on_their_wave(D, span, dtype):
     quiet = q.clone()
     loud = q.clone()
     loud[:, :, 0] += 3.0 * u  # row 0 (and its wave's slow path) rises with the keys
-    outs = [flash_attention(x.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=False)
-            for x in (quiet, loud)]
-    assert torch.equal(outs[0][:, :, 1:span], outs[1][:, :, 1:span])
     ref = flash_attention_ref(loud.to(dtype).float(), k.to(dtype).float(), v.to(dtype).float(), causal=False)
-    assert_close(outs[1], ref, TOL[dtype], f"loud row {dtype}")
+    B = batch_for_two_row_groups(2, L, L, False) if D == 64 else 1  # D=64: the two-row-group kernel
+    k, v = (replicate(x, B).to(dtype).to(DEV) for x in (k, v))
+    outs = [flash_attention(replicate(x, B).to(dtype).to(DEV), k, v, causal=False) for x in (quiet, loud)]
+    assert torch.equal(outs[0][:, :, 1:span], outs[1][:, :, 1:span])
+    assert_close(outs[1], replicate(ref, B), TOL[dtype], f"loud row {dtype}")
 
 
 @pytest.mark.parametrize("D", [64, 128])
@@ -229,9 +276,11 @@ def test_row_max_changes_across_tiles(D, dtype, pattern):
     k = k.to(dtype)
     v = (torch.randn(B, Hk, L, D, generator=g) * 0.5).to(dtype)
     for causal in (True, False):
-        out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal)
         ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=causal)
-        assert_close(out, ref, TOL[dtype], f"{pattern} D={D} {dtype} causal={causal}")
+        # D=64: also repeated over a batch that takes the two-row-group kernel
+        for R in (1, batch_for_two_row_groups(H, L, L, causal)) if D == 64 else (1,):
+            out = flash_attention(replicate(q, R).to(DEV), replicate(k, R).to(DEV), replicate(v, R).to(DEV), causal=causal)
+            assert_close(out, replicate(ref, R), TOL[dtype], f"{pattern} D={D} {dtype} causal={causal} B={R}")
 
 
 def test_deterministic():
