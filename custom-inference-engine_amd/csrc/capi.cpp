@@ -326,6 +326,12 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
     p.plan_empty = (int)L.empty;
     p.info = const_cast<int4*>(reinterpret_cast<const int4*>(p.plan + L.info));  // read only in this mode
     p.slots = static_cast<float*>(workspace);
+    // the merge pass reads its sequences from the plan's merge table, sized by
+    // the split count the plan was built with (capped at the table's size)
+    p.plan_mtab = (int)L.mtab;
+    p.mtab_cap = plan_split > 0 && cie::paged_xcd_runs(g.NG, g.Wg)
+                     ? std::min(cie::merge_cap(plan_split * g.NG), cie::merge_table_cap(B, g.NG))
+                     : 0;
   } else {
     p.info = static_cast<int4*>(workspace);
     p.slots = reinterpret_cast<float*>(static_cast<char*>(workspace) + g.info_bytes);
@@ -359,6 +365,8 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
     p.vs0_24 = (uint32_t)vc_stride[0]; p.vs1_24 = (uint32_t)vc_stride[1];
   }
   p.Hg = g.Hg; p.NG = g.NG; p.n_qt = g.n_qt; p.NWV = g.NWV; p.NCH = g.NCH; p.NST = g.NST; p.Wg = g.Wg;
+  // ranges in XCD runs only where the plan's merge table follows them
+  p.xcd_runs = plan && cie::paged_xcd_runs(g.NG, g.Wg) ? 1 : 0;
   set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
   p.rope = rope;

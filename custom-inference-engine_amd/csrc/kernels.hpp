@@ -68,6 +68,9 @@ struct PagedParams {
   uint32_t ks0_24, ks1_24, vs0_24, vs1_24;
   FastDiv bsdiv;
   FastDiv rtdiv, nwvdiv, ngdiv;  // item decomposition of the merge pass
+  int xcd_runs;   // ranges of a head group in contiguous runs per XCD (paged_xcd_runs)
+  int mtab_cap;   // > 0: the merge pass takes its sequences from the plan's merge table (capacity per XCD)
+  int plan_mtab;  // offset of that table in the plan (int32 elements)
   int Hg, NG, n_qt, NWV, NCH, NST, Wg;
   float scale_log2;  // |scale| * log2(e), never below 1e-30
   uint32_t q_sign;   // 0x80008000 flips the sign of q when the caller's scale is negative
@@ -118,9 +121,33 @@ constexpr int32_t kPlanMagic = 0x43504c31;  // "CPL1"
 constexpr int kPlanHeader = 16;             // header ints
 constexpr int kPlanRangeInts = 8;           // ints per range row
 struct PlanLayout {
-  size_t ranges, entries, ids, info, empty;  // section offsets (int32 elements)
-  size_t ints;                               // total size
+  size_t ranges, entries, ids, info, empty, mtab;  // section offsets (int32 elements)
+  size_t ints;                                     // total size
 };
+// The main pass places the ranges of a head group on the XCDs in contiguous
+// runs (workgroup ids are dispatched round-robin over the 8 XCDs, and each
+// XCD keeps what its workgroups wrote in its L2 across the kernel boundary),
+// and the plan's merge table hands each split sequence's merge work to the
+// XCD holding its pieces: mtab[x][i] (x < 8, i < merge_table_cap(B, NG)) is
+// the i-th sequence (b * NG + gh) merged on XCD x, -1 when unused.
+// Sequences per XCD list: every split sequence fits, with one to spare.
+__host__ __device__ inline int merge_cap(int split_units) { return (split_units + 7) / 8 + 1; }
+__host__ __device__ inline int merge_table_cap(int B, int NG) { return merge_cap(B * NG); }
+// The placement (and the merge table) is used when the main pass has one
+// workgroup per CU or fewer (verify-like shapes: partial states of ~20 query
+// rows per kv head, merge reads from L2 3.8 % faster on verify_b8); with two
+// workgroups per CU (decode-like) contiguous runs cost the main pass more
+// than the merge saves (decode_b32 +1.2 us), and ranges alternate head
+// groups over the workgroup ids instead.
+inline bool paged_xcd_runs(int NG, int Wg) { return (int64_t)NG * Wg <= 256; }
+// XCD of main-pass workgroup `logical` (the order of the remap below) when
+// the grid has n workgroups.
+inline int xcd_of_logical(int64_t logical, int64_t n) {
+  const int64_t base = n >> 3, extra = n & 7;
+  for (int x = 0; x < 7; ++x)
+    if (logical < (x + 1) * base + std::min<int64_t>(x + 1, extra)) return x;
+  return 7;
+}
 PlanLayout paged_plan_layout(const PagedGeom& g, int B, int max_blocks);
 // Fills P (layout L) from host lengths and block tables; returns the number
 // of sequences split across workgroups (>= 0), or -1 when the geometry's

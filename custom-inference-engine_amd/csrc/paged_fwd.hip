@@ -162,8 +162,22 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
   __shared__ int32_t sbt[kPagedIds];
   __shared__ int32_t ent[kPagedEntries][8];  // b, ctx, tt_lo, n, idbase, blk_lo, pre, pieces
 
-  const int gh = blockIdx.x % p.NG;
-  const int j = blockIdx.x / p.NG;
+  // Range j of head group gh. With xcd_runs the ranges of a head group go to
+  // the XCDs in contiguous runs (workgroups are dispatched round-robin over
+  // the 8 XCDs), so the pieces of a split sequence are mostly written through
+  // one XCD's L2, where the merge pass then finds them (merge_table_cap);
+  // otherwise consecutive workgroup ids alternate head groups.
+  int gh, j;
+  if (p.xcd_runs) {
+    const int nwg = p.NG * p.Wg;
+    const int xcd = blockIdx.x & 7, xslot = blockIdx.x >> 3;
+    const int logical = xcd * (nwg >> 3) + min(xcd, nwg & 7) + xslot;
+    gh = logical / p.Wg;
+    j = logical - gh * p.Wg;
+  } else {
+    gh = blockIdx.x % p.NG;
+    j = blockIdx.x / p.NG;
+  }
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, uniform
   const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
   const int hh = w % p.Hg, qt = w / p.Hg;
@@ -737,8 +751,23 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   constexpr int Q4 = D / 4;
   static_assert(kMergeLanes == 8, "the butterfly below covers eight lanes");
   // thread index < 2^31 (paged_geometry bounds the merge grid): 32-bit
-  // decomposition, invariant divisors by multiply-shift
-  const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  // decomposition, invariant divisors by multiply-shift. With the plan's
+  // merge table, workgroup (XCD x, slot s) takes part s % wpu of the x-th
+  // list's sequence s / wpu; otherwise the sequences follow the grid.
+  uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  int unit = -1;
+  if (p.mtab_cap > 0) {
+    // a plan built for other arguments: the main pass has written NaN rows,
+    // and the table's offset may lie past that plan's end
+    if (!plan_matches(p)) return;
+    const uint32_t per_unit = (uint32_t)p.NWV * p.Rt * Q4 * kMergeLanes;
+    const uint32_t wpu = (per_unit + 255) / 256;
+    const uint32_t slot = blockIdx.x >> 3, ui = slot / wpu;
+    if (ui < (uint32_t)p.mtab_cap)
+      unit = p.plan[p.plan_mtab + (int64_t)(blockIdx.x & 7) * merge_table_cap(p.B, p.NG) + ui];
+    if (unit < 0 || unit >= p.B * p.NG) return;  // an unused (or invalid) entry: the whole workgroup idles
+    tid = (slot - ui * wpu) * 256u + threadIdx.x;
+  }
   const int t = (int)(tid % kMergeLanes);
   uint32_t item = tid / kMergeLanes;
   const int d4 = (int)(item % Q4);
@@ -749,12 +778,20 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   qn = fdiv(item, p.nwvdiv);
   const int w = (int)(item - qn * (uint32_t)p.NWV);
   item = qn;
-  qn = fdiv(item, p.ngdiv);
-  const int gh = (int)(item - qn * (uint32_t)p.NG);
-  const int b = (int)qn;
+  int gh, b;
+  bool in;
+  if (unit >= 0) {  // item is 0 within the sequence's threads
+    gh = unit % p.NG;
+    b = unit / p.NG;
+    in = item == 0;
+  } else {
+    qn = fdiv(item, p.ngdiv);
+    gh = (int)(item - qn * (uint32_t)p.NG);
+    b = (int)qn;
+    in = b < p.B;
+  }
   // Items of one wave belong to at most a few sequences; lanes past the end
   // or without work still take part in the shuffles below.
-  const bool in = b < p.B;
   const int4 inf = in ? p.info[(int64_t)gh * p.B + b] : int4{0, 0, 0, 0};
   const int pieces = inf.y;
   const int hh = w % p.Hg, qt = w / p.Hg;
@@ -866,8 +903,10 @@ static hipError_t launch_paged_t(const PagedParams& p, size_t lds, bool merge, h
     hipLaunchKernelGGL((paged_fwd_kernel<DTYPE, D, false>), dim3((unsigned)n_wg), dim3(64 * p.NWV), lds, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !merge) return e;
-  const int64_t threads = (int64_t)p.B * p.NG * p.NWV * p.Rt * (D / 4) * kMergeLanes;
-  hipLaunchKernelGGL((paged_merge_kernel<DTYPE, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
+  const int64_t per_unit = (int64_t)p.NWV * p.Rt * (D / 4) * kMergeLanes;
+  const int64_t n_merge = p.mtab_cap > 0 ? (int64_t)8 * p.mtab_cap * ((per_unit + 255) / 256)
+                                         : ((int64_t)p.B * p.NG * per_unit + 255) / 256;
+  hipLaunchKernelGGL((paged_merge_kernel<DTYPE, D>), dim3((unsigned)n_merge), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

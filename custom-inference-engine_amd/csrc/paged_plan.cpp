@@ -30,6 +30,11 @@
 //            merge pass's piece descriptors), zero for unsplit sequences
 //   empty    B rows of 2: sequences without tiles (b, 1 if the history is
 //            empty, 0 if its length is invalid)
+//   mtab     8 lists of merge_table_cap(B, NG): the split sequences
+//            (b * NG + gh) whose merge runs on each XCD, -1 past the end;
+//            each goes to the XCD that ran its middle piece (its partial
+//            states are in that XCD's L2), or, when that list holds
+//            merge_cap(split sequences) already, to the shortest list
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -46,7 +51,8 @@ PlanLayout paged_plan_layout(const PagedGeom& g, int B, int max_blocks) {
   L.info = L.ids + (size_t)B * max_blocks + (size_t)2 * g.Wg;
   L.info = (L.info + 3) / 4 * 4;  // int4 aligned
   L.empty = L.info + (size_t)4 * g.NG * B;
-  L.ints = L.empty + (size_t)2 * B;
+  L.mtab = L.empty + (size_t)2 * B;
+  L.ints = L.mtab + (size_t)8 * merge_table_cap(B, g.NG);
   return L;
 }
 
@@ -137,6 +143,25 @@ int build_paged_plan(int32_t* P, const PagedGeom& g, const PlanLayout& L, const 
     nid_total += nid;
   }
   (void)max_blocks;
+  // merge table (launches placed in XCD runs only): every split sequence of
+  // every head group, on the XCD of its middle piece when that list has room
+  {
+    const int cap_t = merge_table_cap(B, g.NG), cap = merge_cap(split * g.NG);
+    int32_t* T = P + L.mtab;
+    for (int i = 0; i < 8 * cap_t; ++i) T[i] = -1;
+    if (paged_xcd_runs(g.NG, g.Wg)) {
+    int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int64_t n = (int64_t)g.NG * g.Wg;
+    for (int b = 0; b < B; ++b)
+      for (int gh = 0; gh < g.NG; ++gh) {
+        const int32_t* f = F + (size_t)4 * ((size_t)gh * B + b);
+        if (tiles[b] == 0 || f[1] <= 1) continue;
+        int x = xcd_of_logical((int64_t)gh * g.Wg + f[0] + f[1] / 2, n);
+        if (cnt[x] >= cap) x = (int)(std::min_element(cnt, cnt + 8) - cnt);
+        T[x * cap_t + cnt[x]++] = b * g.NG + gh;
+      }
+    }
+  }
   P[0] = kPlanMagic;
   P[1] = (int32_t)W;
   P[2] = (int32_t)NT;

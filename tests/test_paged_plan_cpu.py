@@ -117,6 +117,37 @@ def _check(lens, bt, Hq, Hk, Lq, D, num_blocks, bs, max_context=None, append=Fal
             assert tuple(f) == info[b], (gh, b, f, info[b])
     n_empty = int(P[4])
     assert [tuple(P[off_z + 2 * z: off_z + 2 * z + 2].tolist()) for z in range(n_empty)] == empty
+    # merge table: 8 lists of cap_t entries; every split sequence of every head
+    # group exactly once, each list at most merge_cap(split * NG) long, each
+    # sequence on the XCD that ran its middle piece unless that list was full
+    off_m = off_z + 2 * B
+    cap_t = (B * NG + 7) // 8 + 1
+    cap = (split * NG + 7) // 8 + 1
+    assert P.numel() == off_m + 8 * cap_t
+    n_wg = NG * Wg
+    base, extra = n_wg // 8, n_wg % 8
+
+    def xcd_of(logical):  # the main pass's XCD of range j of head group gh (logical = gh Wg + j)
+        return next(x for x in range(8) if logical < (x + 1) * base + min(x + 1, extra)) if logical < n_wg else 7
+
+    placed, fallbacks = {}, 0
+    for x in range(8):
+        lst = P[off_m + x * cap_t: off_m + (x + 1) * cap_t].tolist()
+        used = [u for u in lst if u >= 0]
+        assert lst == used + [-1] * (cap_t - len(used)) and len(used) <= cap, (x, lst)
+        for u in used:
+            assert u not in placed, u
+            placed[u] = x
+    # (only launches of one workgroup per CU or fewer place ranges in XCD runs
+    # and fill the table; the others merge in grid order)
+    runs = NG * Wg <= 256
+    want = {b * NG + gh for b in range(B) for gh in range(NG) if info[b][1] > 1} if runs else set()
+    assert set(placed) == want
+    for u, x in placed.items():
+        b, gh = u // NG, u % NG
+        j0, pieces, _ = info[b]
+        fallbacks += xcd_of(gh * Wg + j0 + pieces // 2) != x
+    assert fallbacks <= len(want) // 2, fallbacks  # most sequences land where their pieces are
     return P, split
 
 
