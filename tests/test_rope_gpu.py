@@ -18,6 +18,7 @@ import math
 import pytest
 import torch
 
+from prefill_dispatch import batch_for_two_row_groups, two_row_group_kernel_runs
 from engine.attention import flash_attention, paged_attention
 from engine.cache import KVCacheConfig, PagedKVCache, kv_append
 from engine.model.rope import RotaryEmbedding, build_rope_cache, rope_apply
@@ -172,6 +173,34 @@ def test_rotary_append_position_outside_table_writes_nothing():
     # sequence 1: positions 4, 5 written, 6, 7 not
     blk = tables[1][1]
     assert (vd[blk, :2] == 1).all() and (vd[blk, 2:] == 0).all() and (kd[blk, 2:] == 0).all()
+
+
+@pytest.mark.parametrize("tables", ["fp32", "same"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_flash_with_fused_q_rope_two_row_groups(dtype, tables):
+    """head_dim 64 with enough work runs the two-row-group kernel, which
+    rotates the q rows of both its row groups (two query heads) as they are
+    loaded: equal bit for bit to rope_apply then the same launch, and to the
+    oracle, over a batch of 2 problems repeated (positions from 0 and 300)."""
+    B0, Hq, Hk, L, D = 2, 8, 2, 200, 64
+    c, s, cd, sd = _tables(2048, D, tdt=_tdt(tables, dtype))
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(B0, Hq, L, D, generator=g).to(dtype)
+    k = torch.randn(B0, Hk, L, D, generator=g).to(dtype)
+    v = torch.randn(B0, Hk, L, D, generator=g).to(dtype)
+    pos0 = torch.tensor([0, 300], dtype=torch.int32)
+    kr = torch.cat([rope_ref(k[b:b + 1], c, s, torch.arange(int(pos0[b]), int(pos0[b]) + L)) for b in range(B0)])
+    qr = torch.cat([rope_ref(q[b:b + 1], c, s, torch.arange(int(pos0[b]), int(pos0[b]) + L)) for b in range(B0)])
+    ref = flash_attention_ref(qr.float(), kr.float(), v.float(), causal=True)
+    R = (batch_for_two_row_groups(Hq, L, L, True) + B0 - 1) // B0  # copies of the 2-problem batch
+    B = B0 * R
+    assert two_row_group_kernel_runs(B, Hq, L, L, True)
+    rep = lambda t: t.repeat(R, *([1] * (t.dim() - 1)))  # noqa: E731
+    qd, krd, vd, pd = rep(q).to(DEV), rep(kr).to(DEV), rep(v).to(DEV), rep(pos0).to(DEV)
+    fused = flash_attention(qd, krd, vd, causal=True, rope=(cd, sd), q_pos0=pd)
+    qrd = rep(qr).to(DEV)
+    assert torch.equal(fused, flash_attention(qrd, krd, vd, causal=True))
+    assert (fused.float().cpu() - rep(ref)).abs().max().item() <= TOL[dtype]
 
 
 @pytest.mark.parametrize("tables", ["fp32", "same"])

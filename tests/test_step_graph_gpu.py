@@ -11,6 +11,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from prefill_dispatch import batch_for_two_row_groups, two_row_group_kernel_runs
 from engine.cache import KVCacheConfig, PagedKVCache
 from engine.model import attention_section
 
@@ -74,6 +75,14 @@ def test_out_argument_writes_views_in_place():
     got = flash_attention(q, k, v, causal=True, out=rows.transpose(1, 2))
     assert got.data_ptr() == rows.data_ptr()
     assert torch.equal(rows.transpose(1, 2), flash_attention(q, k, v, causal=True))
+    # 200 rows over a batch that takes the head_dim-64 two-row-group kernel
+    Lr = 200
+    Br = batch_for_two_row_groups(Hq, Lr, Lr, True)
+    assert two_row_group_kernel_runs(Br, Hq, Lr, Lr, True)
+    qr, kr, vr = (torch.randn(Br, h, Lr, D, generator=g).half().to(DEV) for h in (Hq, Hk, Hk))
+    big = torch.full((Br, Lr, Hq, D), 7.0, dtype=torch.float16, device=DEV)
+    flash_attention(qr, kr, vr, causal=True, out=big.transpose(1, 2))
+    assert torch.equal(big.transpose(1, 2), flash_attention(qr, kr, vr, causal=True))
     cache = PagedKVCache(KVCacheConfig(num_layers=1, num_kv_heads=Hk, head_dim=D, num_blocks=64, block_size=16,
                                        dtype=torch.float16, device=DEV))
     tables = [cache.new_sequence() for _ in range(B)]
