@@ -8,10 +8,10 @@
 //
 // Memory path: each K/V tile (BN keys) is copied global -> LDS by 16-byte
 // direct-to-LDS loads issued by all four waves (no VGPR staging), row-major
-// with the 16-byte chunks of each row XOR-swizzled (chunk_swizzle). Up to two tiles are in
-// flight while the tiles being read stay resident; one workgroup barrier per
-// tile (four stages), or per two tiles at D=128 (five stages), publishes the
-// next tile(s) and frees the stage(s) refilled next.
+// with the 16-byte chunks of each row XOR-swizzled (chunk_swizzle). One or
+// two tiles are in flight while the tiles being read stay resident; one
+// workgroup barrier per tile publishes the next tile and frees the stage
+// refilled next (three or four stages).
 // Per tile and wave:
 //   S^T[BN x 32] = K_tile . Q_w^T - m MFMA 32x32x16; A = ds_read_b128 of K rows,
 //                                      B = Q^T resident in registers, scaled by
@@ -485,7 +485,7 @@ struct IlCfg {
   static constexpr int NCC = 2 * MT;             // 16-key blocks of P per tile
   static constexpr int TILE = BN * D;
   static constexpr int STAGE = 2 * TILE;         // K tile, then V tile
-  static constexpr int NST = 5;                  // ring stages
+  static constexpr int NST = 4;                  // ring stages (one tile in flight; S=16384 1760 -> 1744 us against five)
   static constexpr int AHEAD = NST - 3;          // tiles in flight behind the one a barrier publishes
   static constexpr int NW = BN * S / 256;        // 1 KiB copies per wave per tensor
   static constexpr int PER_TILE = 2 * NW;
