@@ -459,7 +459,8 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
   if (p.rope.cos) {  // RoPE fused into the load: row i at position ctx - Lq + i
 #pragma unroll
     for (int e = 0; e < C::QPRE; ++e)
-      rope_q_lane<DTYPE, D>(qpre[e], p.rope, (e < ne ? ent[e][1] : 0) - p.Lq + i, rv && e < ne, hl);
+      if (e < ne)  // wave-uniform: preload slots past the range's sequences hold zeros and are never used
+        rope_q_lane<DTYPE, D>(qpre[e], p.rope, ent[e][1] - p.Lq + i, rv, hl);
   }
 #pragma unroll
   for (int e = 0; e < C::QPRE; ++e)
