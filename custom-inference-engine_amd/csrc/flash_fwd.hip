@@ -960,6 +960,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
 #pragma unroll
       for (int rg = 0; rg < NRG; ++rg) {
         live[rg] = qi[rg] < p.Lq;
+        // (this kernel runs only with Lq > 128, so row Lq - 1 exists)
         const uint16_t* qrow = p.q + b * p.qs0 + hq[rg] * p.qs1 + (int64_t)min(qi[rg], p.Lq - 1) * p.qs2;
 #pragma unroll
         for (int kk = 0; kk < C::KK; ++kk) qf[rg][kk] = load16_clamped(qrow + 16 * kk + 8 * hl);
