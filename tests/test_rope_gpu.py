@@ -203,6 +203,61 @@ def test_flash_with_fused_q_rope_two_row_groups(dtype, tables):
     assert (fused.float().cpu() - rep(ref)).abs().max().item() <= TOL[dtype]
 
 
+def _equal_or_both_nan(a, b):
+    """NaN in the same places and equal bit for bit everywhere else."""
+    an, bn = torch.isnan(a), torch.isnan(b)
+    return torch.equal(an, bn) and torch.equal(a[~an], b[~bn])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_flash_fused_q_rope_positions_past_the_table(dtype):
+    """Through the two-row-group kernel: a row whose position lies past the
+    rotary tables comes out NaN (the reference's table indexing raises there)
+    and every other row is what rope_apply then the same launch gives."""
+    B0, Hq, Hk, L, D, rows = 2, 8, 2, 200, 64, 1024
+    _, _, cd, sd = _tables(rows, D)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B0, Hq, L, D, generator=g).to(dtype)
+    k = (torch.randn(B0, Hk, L, D, generator=g) * 0.125).to(dtype)
+    v = torch.randn(B0, Hk, L, D, generator=g).to(dtype)
+    pos0 = torch.tensor([0, rows - 150], dtype=torch.int32)  # batch 1: rows 150.. lie past the table
+    R = (batch_for_two_row_groups(Hq, L, L, True) + B0 - 1) // B0
+    assert two_row_group_kernel_runs(B0 * R, Hq, L, L, True)
+    rep = lambda t: t.repeat(R, *([1] * (t.dim() - 1)))  # noqa: E731
+    qd, kd, vd, pd = rep(q).to(DEV), rep(k).to(DEV), rep(v).to(DEV), rep(pos0).to(DEV)
+    fused = flash_attention(qd, kd, vd, causal=True, rope=(cd, sd), q_pos0=pd)
+    pos = pd[:, None].long() + torch.arange(L, device=DEV)[None]
+    unfused = flash_attention(rope_apply(qd, cd, sd, pos), kd, vd, causal=True)
+    assert _equal_or_both_nan(fused, unfused)
+    nan_rows = torch.isnan(fused.float()).all(-1)
+    assert torch.equal(nan_rows, (pos >= rows)[:, None, :].expand_as(nan_rows))
+    assert torch.isfinite(fused.float()[~nan_rows]).all()
+
+
+@pytest.mark.parametrize("Lq,dtype", [(1, torch.float16), (5, torch.bfloat16)])
+def test_paged_fused_q_rope_positions_past_the_table(Lq, dtype):
+    """Paged: new-token rows at positions past the rotary tables come out NaN,
+    the others equal rope_apply then the same launch."""
+    Hq, Hk, D, bs, rows = 8, 2, 64, 16, 1024
+    ctx = [40, rows + 6, 5 + Lq, rows + Lq - 1, 333]
+    B = len(ctx)
+    _, _, cd, sd = _tables(rows, D)
+    nb, _, bt = _batch_tables(ctx, [0] * B, bs, seed=Lq)
+    g = torch.Generator().manual_seed(Lq)
+    kp = torch.randn(nb, bs, Hk, D, generator=g).to(dtype)
+    vp = torch.randn(nb, bs, Hk, D, generator=g).to(dtype)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(dtype)
+    qd, kd, vd, btd = q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV)
+    ld = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    fused = paged_attention(qd, kd, vd, btd, ld, causal=True, rope=(cd, sd))
+    pos = torch.stack([torch.arange(n - Lq, n) for n in ctx]).to(DEV)
+    unfused = paged_attention(rope_apply(qd, cd, sd, pos), kd, vd, btd, ld, causal=True)
+    assert _equal_or_both_nan(fused, unfused)
+    nan_rows = torch.isnan(fused.float()).all(-1)
+    assert torch.equal(nan_rows, (pos >= rows)[:, None, :].expand_as(nan_rows))
+    assert nan_rows.any() and not nan_rows.all()
+
+
 @pytest.mark.parametrize("tables", ["fp32", "same"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("D", [16, 64, 128])
