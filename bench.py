@@ -602,7 +602,7 @@ def main():
     import torch
 
     from benchmarks import workloads
-    from engine.attention import flash_attention
+    from engine.attention import flash_attention, prefill_kernel
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -610,10 +610,20 @@ def main():
     q, k, v = case.q.to(dev), case.k.to(dev), case.v.to(dev)
 
     # Launches of the prefill kernel are counted in launch order, so a kernel
-    # trace of this run can pick out the timed ones. At head_dim 64 with an
-    # even group size it is the head-pair kernel: one workgroup per 128-row
-    # query tile and pair of query heads.
-    prefill_wg = ((case.q.shape[2] + 127) // 128) * case.q.shape[0] * case.q.shape[1] // 2
+    # trace of this run can pick out the timed ones. The library names the
+    # kernel this shape takes (on an MI355X the head-pair kernel: one
+    # workgroup per 128-row query tile and pair of query heads).
+    B_, H_, S_, D_ = case.q.shape
+    kind = prefill_kernel(B_, H_, case.k.shape[1], S_, case.k.shape[2], D_, True, case.q.dtype)
+    n_mt = (S_ + 127) // 128
+    kernel_names = {
+        "r64_heads": ("cie::flash_fwd_r64_kernel<0, 64, true>", "flash_fwd_r64_kernel<fp16, D=64, head pairs>",
+                      n_mt * B_ * H_ // 2),
+        "r64_rows": ("cie::flash_fwd_r64_kernel<0, 64, false>", "flash_fwd_r64_kernel<fp16, D=64, 64-row waves>",
+                     ((S_ + 255) // 256) * B_ * H_),
+        "flash_fwd": ("cie::flash_fwd_kernel<0, 64>", "flash_fwd_kernel<fp16, D=64>", n_mt * B_ * H_),
+    }
+    trace_name, roof_name, prefill_wg = kernel_names[kind]
     launches = [0]
 
     def headline(i=0):
@@ -644,13 +654,13 @@ def main():
     n_roof = max(20, args.steps)
     kern_ms = event_time_ms(roof, n_roof, 3, mark=lambda: launches[0])
     print("[bench-launches] " + json.dumps({
-        "kernel": "cie::flash_fwd_r64_kernel<0, 64, true>", "workgroups": prefill_wg, "workload": "prefill_s2048",
+        "kernel": trace_name, "workgroups": prefill_wg, "workload": "prefill_s2048",
         "headline_steps": [first_timed, args.steps],
         "roofline_trials": [[m, n_roof] for m in event_time_ms.marks]}), file=sys.stderr, flush=True)
     achieved = case.flops / (kern_ms / 1e3) / 1e12
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": traffic_from_summary(),
-            "kernel": "flash_fwd_r64_kernel<fp16, D=64, head pairs>", "kernel_us": round(kern_ms * 1e3, 2)}
+            "kernel": roof_name, "kernel_us": round(kern_ms * 1e3, 2)}
 
     extra = {}
     if not args.no_extra:

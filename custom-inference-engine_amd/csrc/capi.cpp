@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdarg>
+#include <map>
 #include <mutex>
 #include <set>
 #include <string>
@@ -17,6 +18,35 @@
 #include "kernels.hpp"
 
 namespace cie {
+
+DeviceShape shape_for_cus(int cus) {
+  if (cus < 1) cus = kDefaultCUs;
+  const int xcds = std::min(std::max(cus / 32, 1), kMaxXcds);  // 32 active CUs per gfx950 XCD
+  int shift = 0;
+  while ((2 << shift) <= xcds) ++shift;
+  return DeviceShape{cus, shift};
+}
+
+DeviceShape device_shape() {
+  static std::mutex mu;
+  static std::map<int, DeviceShape> known;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();  // no device: leave no error behind for a later launch check
+    return shape_for_cus(kDefaultCUs);
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = known.find(dev);
+  if (it == known.end()) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) {
+      (void)hipGetLastError();
+      cus = kDefaultCUs;
+    }
+    it = known.emplace(dev, shape_for_cus(cus)).first;
+  }
+  return it->second;
+}
 
 hipError_t set_dynamic_lds(const void* kernel, int bytes) {
   static std::mutex mu;
@@ -118,6 +148,25 @@ int cie_abi_version(void) { return CIE_ABI_VERSION; }
 
 const char* cie_last_error(void) { return g_err.c_str(); }
 
+int cie_device_cus(void) { return cie::device_shape().cus; }
+
+int cie_prefill_kernel(int B, int Hq, int Hk, int Lq, int Lk, int D, int causal, int dtype, int cu_count) {
+  CIE_TRY(common_checks(Hq, Hk, D, dtype));
+  if (B < 0 || Lq < 0 || Lk < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d, Lk=%d)", B, Lq, Lk);
+  const int64_t n_mt = ((int64_t)Lq + 127) / 128;
+  if (n_mt * B * Hq > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
+  cie::FlashParams p{};
+  p.B = B; p.Hq = Hq; p.Hk = Hk; p.Lq = Lq; p.Lk = Lk; p.group = Hq / Hk;
+  p.n_mt = (int)n_mt;
+  p.n_wg = (int)(n_mt * B * Hq);
+  p.causal = causal ? 1 : 0;
+  const cie::DeviceShape dev = cu_count > 0 ? cie::shape_for_cus(cu_count) : cie::device_shape();
+  p.cus = dev.cus;
+  p.xcd_shift = dev.xcd_shift;
+  g_err.clear();
+  return (int)cie::flash_kernel_choice(p, D);
+}
+
 }  // extern "C"
 
 static int flash_impl(const void* q, const void* k, const void* v, void* o,
@@ -165,6 +214,9 @@ static int flash_impl(const void* q, const void* k, const void* v, void* o,
   p.causal = causal ? 1 : 0;
   p.rope = rope;
   p.q_pos0 = q_pos0;
+  const cie::DeviceShape dev = cie::device_shape();
+  p.cus = dev.cus;
+  p.xcd_shift = dev.xcd_shift;
   return launch_status(cie::launch_flash(p, dtype, D, static_cast<hipStream_t>(stream)));
 }
 
@@ -203,8 +255,8 @@ size_t cie_paged_workspace_bytes(int B, int Hq, int Hk, int Lq, int D, int max_c
       Hq % Hk)
     return 0;
   if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff) return 0;
-  const cie::PagedGeom g =
-      cie::paged_geometry(B, Hq, Hk, Lq, D, paged_ctx_limit(max_context, block_size, max_blocks_per_seq), block_size);
+  const cie::PagedGeom g = cie::paged_geometry(
+      B, Hq, Hk, Lq, D, paged_ctx_limit(max_context, block_size, max_blocks_per_seq), block_size, cie::device_shape());
   return g.ok ? g.info_bytes + g.slot_bytes : 0;
 }
 
@@ -214,8 +266,8 @@ size_t cie_paged_plan_bytes(int B, int Hq, int Hk, int Lq, int D, int max_contex
       Hq % Hk)
     return 0;
   if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff) return 0;
-  const cie::PagedGeom g =
-      cie::paged_geometry(B, Hq, Hk, Lq, D, paged_ctx_limit(max_context, block_size, max_blocks_per_seq), block_size);
+  const cie::PagedGeom g = cie::paged_geometry(
+      B, Hq, Hk, Lq, D, paged_ctx_limit(max_context, block_size, max_blocks_per_seq), block_size, cie::device_shape());
   if (!g.ok) return 0;
   const cie::PlanLayout L = cie::paged_plan_layout(g, B, max_blocks_per_seq);
   if (L.ints > 0x7fffffff) return 0;
@@ -233,7 +285,7 @@ int cie_paged_plan(void* plan, size_t plan_bytes, const int32_t* context_lens, c
   if (need == 0) return fail(CIE_EINVAL, "plan: unsupported shape");
   if (plan_bytes < need) return fail(CIE_EWORKSPACE, "plan: %zu bytes required, %zu given", need, plan_bytes);
   const int ctx_limit = paged_ctx_limit(max_context, block_size, max_blocks_per_seq);
-  const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size);
+  const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size, cie::device_shape());
   const cie::PlanLayout L = cie::paged_plan_layout(g, B, max_blocks_per_seq);
   const int split = cie::build_paged_plan(static_cast<int32_t*>(plan), g, L, context_lens, block_tables,
                                           block_table_row_stride, B, Lq, num_blocks, block_size,
@@ -297,7 +349,7 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
 
   const int ctx_limit = paged_ctx_limit(max_context, block_size, max_blocks_per_seq);
   if ((int64_t)B * ((ctx_limit + 31) / 32) > 0x7fffffff) return fail(CIE_EINVAL, "problem too large for one launch");
-  const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size);
+  const cie::PagedGeom g = cie::paged_geometry(B, Hq, Hk, Lq, D, ctx_limit, block_size, cie::device_shape());
   if (!g.ok) return fail(CIE_EINVAL, "paged attention: %s", g.err);
   // with a plan the piece descriptors live in the plan; the workspace holds
   // only the partial states, and none at all when no sequence is split
@@ -329,8 +381,10 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
     // the merge pass reads its sequences from the plan's merge table, sized by
     // the split count the plan was built with (capped at the table's size)
     p.plan_mtab = (int)L.mtab;
-    p.mtab_cap = plan_split > 0 && cie::paged_xcd_runs(g.NG, g.Wg)
-                     ? std::min(cie::merge_cap(plan_split * g.NG), cie::merge_table_cap(B, g.NG))
+    p.plan_split = plan_split;
+    p.mtab_cap = plan_split > 0 && cie::paged_xcd_runs(g)
+                     ? std::min(cie::merge_cap(plan_split * g.NG, g.dev.xcd_shift),
+                                cie::merge_table_cap(B, g.NG, g.dev.xcd_shift))
                      : 0;
   } else {
     p.info = static_cast<int4*>(workspace);
@@ -366,7 +420,8 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   }
   p.Hg = g.Hg; p.NG = g.NG; p.n_qt = g.n_qt; p.NWV = g.NWV; p.NCH = g.NCH; p.NST = g.NST; p.Wg = g.Wg;
   // ranges in XCD runs only where the plan's merge table follows them
-  p.xcd_runs = plan && cie::paged_xcd_runs(g.NG, g.Wg) ? 1 : 0;
+  p.xcd_runs = plan && cie::paged_xcd_runs(g) ? 1 : 0;
+  p.xcd_shift = g.dev.xcd_shift;
   set_scale(scale, &p.scale_log2, &p.q_sign);
   p.causal = causal ? 1 : 0;
   p.rope = rope;
@@ -601,7 +656,7 @@ int cie_kv_append_rope(const void* k_new, const void* v_new, void* k_cache, void
 
 size_t cie_int8_matmul_workspace_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return cie::int8_gemm_geometry(M, N, K).workspace_bytes;
+  return cie::int8_gemm_geometry(M, N, K, cie::device_shape()).workspace_bytes;
 }
 
 int cie_int8_matmul(const void* x, const int8_t* w, const void* scales, const void* bias, void* y,
@@ -631,7 +686,7 @@ int cie_int8_matmul(const void* x, const int8_t* w, const void* scales, const vo
     return fail(CIE_EINVAL, "w_int8 row stride %lld must be >= K and a multiple of 16 bytes",
                 (long long)w_row_stride);
   if (y_row_stride < N) return fail(CIE_EINVAL, "y row stride %lld must be >= N", (long long)y_row_stride);
-  const cie::I8Geom g = cie::int8_gemm_geometry(M, N, K);
+  const cie::I8Geom g = cie::int8_gemm_geometry(M, N, K, cie::device_shape());
   if ((int64_t)g.n_tiles * g.m_tiles * g.splits > 0x7fffffff) return fail(CIE_EINVAL, "problem too large");
   if (g.workspace_bytes) {
     if (!workspace || workspace_bytes < g.workspace_bytes)
@@ -652,6 +707,7 @@ int cie_int8_matmul(const void* x, const int8_t* w, const void* scales, const vo
   p.M = M; p.N = N; p.K = K; p.scale_dtype = scale_dtype;
   p.n_tiles = g.n_tiles; p.m_tiles = g.m_tiles; p.splits = g.splits; p.ksteps = g.ksteps;
   p.m_pad = g.m_pad; p.n_pad = g.n_pad;
+  p.xcd_shift = g.dev.xcd_shift;
   return launch_status(cie::launch_int8_gemm(p, g, dtype, static_cast<hipStream_t>(stream)));
 }
 

@@ -13,12 +13,10 @@
 // workgroup barrier per tile publishes the next tile and frees the stage
 // refilled next (three or four stages).
 // Per tile and wave:
-//   S^T[BN x 32] = K_tile . Q_w^T - m MFMA 32x32x16; A = ds_read_b128 of K rows,
-//                                      B = Q^T resident in registers, scaled by
-//                                      c = scale*log2e; one more k-block holds
-//                                      a constant column (A) against -m (B)
-//   p = exp2(s)                        the whole softmax argument comes out of
-//                                      the MFMA: no per-score VALU arithmetic
+//   S^T[BN x 32] = K_tile . Q_w^T     MFMA 32x32x16; A = ds_read_b128 of K rows,
+//                                      B = Q^T resident in registers (unscaled)
+//   p = exp2(s * c - m)                one fma per score on the fp32
+//                                      accumulator, c = scale * log2 e
 //   O^T[D x 32] += V^T_tile . P^T      MFMA 32x32x16; A = ds_read_b64_tr_b16 of
 //                                      the row-major V tile, B = P^T straight
 //                                      from the S^T registers
@@ -27,18 +25,19 @@
 // wave's diagonal or the key tail; a workgroup stops at the last key any of
 // its rows can see (the n_end bound of kernels/flash_attention.py:75-77).
 //
-// Q is scaled by c once, as it is loaded, and rounded to the input type
-// (relative error 2^-11 for fp16, 2^-8 for bf16 per element, far inside the
-// output tolerances; c * q must be finite in the input type); m is kept at a
-// value the 16-bit B operand holds exactly. The running max is refreshed
-// lazily and without a per-tile row max: p(t) is computed against the
-// reference max m, and only when a row's probabilities of the tile sum past
-// 2^10 (so some p may not fit the 16-bit P.V operand; always the case for a
-// row that had no visible key before) does the wave recompute S(t) from the
-// still-resident K tile, take its row max, raise m to it and redo the tile.
-// Otherwise every p <= 2^10, exact to fp16 / bf16 rounding. The final acc / l
-// is unchanged by the choice of m. l accumulates the probabilities as rounded
-// for the P.V product, summed on the matrix pipe (see sum_ones).
+// The softmax scale is applied to the fp32 score accumulator, as the
+// reference applies it to the fp32 dot product (kernels/flash_attention.py:
+// 98): q enters the MFMA exactly as given (a negative scale flips its sign,
+// which is exact), so no rounding of scale * q to 16 bits enters the scores.
+// The running max is refreshed lazily and without a per-tile row max: p(t)
+// is computed against the reference max m, and only when a row's
+// probabilities of the tile sum past 2^10 (so some p may not fit the 16-bit
+// P.V operand; always the case for a row that had no visible key before)
+// does the wave recompute S(t) from the still-resident K tile, take its row
+// max, raise m to it and redo the tile. Otherwise every p <= 2^10, exact to
+// fp16 / bf16 rounding. The final acc / l is unchanged by the choice of m. l
+// accumulates the probabilities as rounded for the P.V product, summed on
+// the matrix pipe (see sum_ones).
 //
 // The tile loop is unrolled by a multiple of the ring depth so that every
 // LDS stage offset is an immediate of the fragment reads.
@@ -71,17 +70,6 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-// The two 16-bit values of a packed pair as floats (exact).
-template <int DTYPE>
-__device__ __forceinline__ f32x2 unpack2(uint32_t v) {
-  if constexpr (DTYPE == 0) {
-    const f16x2 h = __builtin_bit_cast(f16x2, v);
-    return f32x2{(float)h[0], (float)h[1]};
-  } else {
-    return f32x2{__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u)};
-  }
 }
 
 template <int D>
@@ -118,13 +106,11 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   constexpr int BN = C::BN;
   __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
 
-  // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
+  // Workgroups are dispatched round-robin over the XCDs; give each XCD a
   // contiguous run of logical tiles so the query heads of a kv head (and its
   // neighbouring query tiles) share one L2. Within a kv head the longest
   // (last) query tiles go first.
-  const int N = p.n_wg;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int logical = xcd * (N >> 3) + min(xcd, N & 7) + slot;
+  const int logical = xcd_logical(blockIdx.x, p.n_wg, p.xcd_shift);
   const int G = p.group;
   const int per_grp = p.n_mt * G;
   const int grp = logical / per_grp;
@@ -138,8 +124,9 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   const int q0w = mt * C::BM + wave * 32;  // first row of this wave
   const int qi = q0w + l32;                // row owned by this lane
 
-  // Q^T as the B operand: lane holds c * Q[qi][16kk + 8hl .. +8] (c takes the
-  // sign of the caller's scale; p.scale_log2 itself is never negative).
+  // Q^T as the B operand: lane holds Q[qi][16kk + 8hl .. +8], its sign
+  // flipped when the caller's scale is negative (p.scale_log2 is |scale| *
+  // log2 e, never negative).
   const uint16_t* qrow = p.q + b * p.qs0 + hq * p.qs1 + (int64_t)qi * p.qs2;
   u32x4 qf[C::KK];
 #pragma unroll
@@ -147,16 +134,8 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   if (p.rope.cos)  // RoPE fused into the load: row qi at position q_pos0[b] + qi
     rope_q_lane<DTYPE, D>(qf, p.rope, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq, hl);
   const float c = p.scale_log2;
-  {
-    const float cq = p.q_sign ? -c : c;
 #pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const f32x2 v = unpack2<DTYPE>(qf[kk][w]);
-        qf[kk][w] = E::pack2(v[0] * cq, v[1] * cq);
-      }
-  }
+  for (int kk = 0; kk < C::KK; ++kk) qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
 
   // Key range of the workgroup and of this wave; lim = last key this row sees.
   const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;
@@ -258,19 +237,12 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
   f32x16 acc[C::DT];
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f;
-  // Extra k-block of the QK^T product: A[key][0] = kMScale, B[0][row] =
-  // -m / kMScale, every other entry 0, so the accumulator starts at -m.
-  constexpr float kMScale = DTYPE == 0 ? 256.f : 1.f;  // fp16 range for |m| up to 2^24
-  const u32x4 a_one = {hl == 0 ? E::pack2(kMScale, 0.f) : 0u, 0u, 0u, 0u};
-  u32x4 b_m = {0u, 0u, 0u, 0u};
-  auto set_m = [&](float x) CIE_INLINE {  // m = x rounded to what the B operand holds exactly
-    if (x != -INFINITY) {
-      x = fminf(x, 65504.f * kMScale);
-      x = unpack2<DTYPE>(E::pack2(x * (1.f / kMScale), 0.f))[0] * kMScale;
-    }
+  // m: the row's reference max in the exp2 domain (c * s), -inf until the
+  // row has a visible key; nm = -m, or 0 while m is -inf.
+  float m = -INFINITY, l = 0.f, nm = 0.f;
+  auto set_m = [&](float x) CIE_INLINE {
     m = x;
-    b_m[0] = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
+    nm = x == -INFINITY ? 0.f : -x;
   };
   // Row sums of P: 4x4x4 MFMAs (16 blocks) with A all ones add four packed
   // p of a lane into that lane's accumulator and nothing else (a p that is
@@ -293,10 +265,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     __syncthreads();
     qk(0, sc);
     mask(0, sc);
-    set_m(xhalf_max(rowmax(sc)));  // the reference max starts at tile 0's row max
-    const float sub = m == -INFINITY ? 0.f : m;
-#pragma unroll
-    for (int mt2 = 0; mt2 < C::MT; ++mt2) sc[mt2] -= sub;
+    set_m(xhalf_max(rowmax(sc)) * c);  // the reference max starts at tile 0's row max
   }
   const int rq = lane & 15, gq = lane >> 4;  // transpose-read lane coordinates
   // One pipeline step: sc holds S(t), S(t+1) is produced in sn; ST is the
@@ -335,7 +304,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
         ka[i] = *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
       }
 #pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = E::mfma(a_one, b_m, f32x16{});
+      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = f32x16{};
       constexpr int EPC = 16 * C::MT / C::NQK;  // S(t) elements per MFMA
 #pragma unroll
       for (int i = 0; i < C::NQK; ++i) {
@@ -345,7 +314,7 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
 #pragma unroll
         for (int e = i * EPC; e < (i + 1) * EPC; ++e) {
           const int m2 = e / 16, ee = e % 16;
-          sc[m2][ee] = exp2_fast(sc[m2][ee]);
+          sc[m2][ee] = exp2_fast(fmaf(sc[m2][ee], c, nm));
           if (ee & 1) {  // a pair is complete: pack it
             const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
             asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
@@ -354,8 +323,8 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
           // four p of P(t) are packed: their sum on the matrix pipe (a DOT
           // instruction per pair would wait for the pipe to drain)
           if ((ee & 3) == 3) {
-            const int c = 2 * m2 + (ee >> 3), w = (ee & 7) >> 1;
-            tsm[(ee >> 2) & 1] = E::mfma4(sum_ones, u32x2{pb[c][w - 1], pb[c][w]}, tsm[(ee >> 2) & 1]);
+            const int cb = 2 * m2 + (ee >> 3), w = (ee & 7) >> 1;
+            tsm[(ee >> 2) & 1] = E::mfma4(sum_ones, u32x2{pb[cb][w - 1], pb[cb][w]}, tsm[(ee >> 2) & 1]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -369,23 +338,19 @@ __global__ __launch_bounds__(256, FlashCfg<D>::OCC) void flash_fwd_kernel(const 
     // to the row max, accumulators rescaled, the tile's p recomputed.
     float ts = xhalf_sum(tsm[0][0] + tsm[1][0]);  // the row's sum of the tile's p
     if (__builtin_amdgcn_ballot_w64(!(ts <= kSumTrigger))) {
-      const float m_in = m == -INFINITY ? 0.f : m;  // subtracted from S(t+1) in sn
       qk(t, sc);
       mask(t, sc);
       const float m_old = m;
-      set_m(maxf(m, xhalf_max(rowmax(sc))));
+      set_m(maxf(m, xhalf_max(rowmax(sc)) * c));
       const float alpha = m > m_old ? exp2_fast(m_old - m) : 1.f;  // 0 when m was -inf
       l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
-      const float nm = m == -INFINITY ? 0.f : -m;
-#pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] += m_in + nm;
 #pragma unroll
       for (int e = 0; e < 16 * C::MT; e += 2) {
         const int m2 = e / 16, ee = e % 16;
         pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] =
-            E::pack2(exp2_fast(sc[m2][ee] + nm), exp2_fast(sc[m2][ee + 1] + nm));
+            E::pack2(exp2_fast(fmaf(sc[m2][ee], c, nm)), exp2_fast(fmaf(sc[m2][ee + 1], c, nm)));
       }
       tsm[0] = tsm[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -489,7 +454,7 @@ struct IlCfg {
   static constexpr int AHEAD = NST - 3;          // tiles in flight behind the one a barrier publishes
   static constexpr int NW = BN * S / 256;        // 1 KiB copies per wave per tensor
   static constexpr int PER_TILE = 2 * NW;
-  static constexpr int NQK = KK * MT;            // QK^T MFMAs per tile (plus the -m block)
+  static constexpr int NQK = KK * MT;            // QK^T MFMAs per tile
   static constexpr int NPV = DT * NCC;           // P.V MFMAs per tile
   static constexpr int NE = 16 * MT;             // scores per lane per tile
   static constexpr int EPC = NE / (2 * NQK);     // scores per VALU chunk
@@ -523,9 +488,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
   constexpr int BN = C::BN;
   __shared__ __attribute__((aligned(16))) uint16_t ring[C::NST * C::STAGE];
 
-  const int N = p.n_wg;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int logical = xcd * (N >> 3) + min(xcd, N & 7) + slot;
+  const int logical = xcd_logical(blockIdx.x, p.n_wg, p.xcd_shift);
   const int G = p.group;
   const int per_grp = p.n_mt * G;
   const int grp = logical / per_grp;
@@ -544,17 +507,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
 #pragma unroll
   for (int kk = 0; kk < C::KK; ++kk) qf[kk] = load16(qrow + 16 * kk + 8 * hl, qi < p.Lq);
   if (p.rope.cos) rope_q_lane<DTYPE, D>(qf, p.rope, (p.q_pos0 ? p.q_pos0[b] : 0) + qi, qi < p.Lq, hl);
-  {
-    const float c = p.scale_log2;
-    const float cq = p.q_sign ? -c : c;
 #pragma unroll
-    for (int kk = 0; kk < C::KK; ++kk)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const f32x2 v = unpack2<DTYPE>(qf[kk][w]);
-        qf[kk][w] = E::pack2(v[0] * cq, v[1] * cq);
-      }
-  }
+  for (int kk = 0; kk < C::KK; ++kk) qf[kk] ^= u32x4{p.q_sign, p.q_sign, p.q_sign, p.q_sign};
+  const float c = p.scale_log2;
 
   const int wg_last_row = min(p.Lq, mt * C::BM + C::BM) - 1;
   int kend = p.Lk;
@@ -615,7 +570,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
     const int sl = (2 * kk + hl) ^ chunk_swizzle<C::S>(row);
     return *reinterpret_cast<const u32x4*>(ks + (row * C::S + sl) * 8);
   };
-  // S^T of the tile in stage ks (no -m block).
+  // S^T of the tile in stage ks.
   auto qk = [&](const uint16_t* ks, f32x16* s) CIE_INLINE {
 #pragma unroll
     for (int mt2 = 0; mt2 < C::MT; ++mt2) s[mt2] = f32x16{};
@@ -657,17 +612,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
   f32x16 acc[C::DT];
 #pragma unroll
   for (int dt = 0; dt < C::DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f;  // l: the row's sum over both lanes
-  uint32_t bm = 0u;  // word 0 of the -m block's B operand
-  constexpr float kMScale = DTYPE == 0 ? 256.f : 1.f;  // fp16 range for |m| up to 2^24
-  const u32x4 a_one = {hl == 0 ? E::pack2(kMScale, 0.f) : 0u, 0u, 0u, 0u};
-  auto set_m = [&](float x) CIE_INLINE {  // m = x rounded to what the B operand holds exactly
-    if (x != -INFINITY) {
-      x = fminf(x, 65504.f * kMScale);
-      x = unpack2<DTYPE>(E::pack2(x * (1.f / kMScale), 0.f))[0] * kMScale;
-    }
+  // m: the row's reference max in the exp2 domain (c * s); nm = -m, or 0
+  // while m is -inf. l: the row's sum over both lanes.
+  float m = -INFINITY, l = 0.f, nm = 0.f;
+  auto set_m = [&](float x) CIE_INLINE {
     m = x;
-    bm = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
+    nm = x == -INFINITY ? 0.f : -x;
   };
   // Row sums of P: 4x4x4 MFMAs with A all ones (see flash_fwd_kernel).
   const u32x2 sum_ones = {E::pack2(1.f, 1.f), E::pack2(1.f, 1.f)};
@@ -683,41 +633,33 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
     __syncthreads();
     qk(ring, sA);
     mask(0, sA);
-    set_m(rowmax(sA));  // the reference max starts at tile 0's row max
-    const float sub = m == -INFINITY ? 0.f : m;
-#pragma unroll
-    for (int mt2 = 0; mt2 < C::MT; ++mt2) sA[mt2] -= sub;
+    set_m(rowmax(sA) * c);  // the reference max starts at tile 0's row max
   }
 
   // Lazy-max check of tile tc (its P in pq, its row sum of p in ts; K(tc)
-  // in stage kst; sx = S(tc+1) - m). A row whose sum
-  // passed 2^10 (some p may not fit the 16-bit P.V operand; always the case
-  // for a row that had no visible key before) recomputes S(tc) from the
-  // resident K tile, raises m to its row max, rescales O and l, and redoes
-  // its p; the other rows keep theirs.
-  auto check = [&](const int tc, const uint16_t* kst, u32x4* pq, f32x16* sx, float ts) CIE_INLINE {
+  // in stage kst). A row whose sum passed 2^10 (some p may not fit the
+  // 16-bit P.V operand; always the case for a row that had no visible key
+  // before) recomputes S(tc) from the resident K tile, raises m to its row
+  // max, rescales O and l, and redoes its p; the other rows keep theirs.
+  auto check = [&](const int tc, const uint16_t* kst, u32x4* pq, float ts) CIE_INLINE {
     const bool trig = !(ts <= kSumTrigger);
     if (__builtin_amdgcn_ballot_w64(trig)) {
       f32x16 s2[C::MT];
       qk(kst, s2);
       mask(tc, s2);
-      const float mx = rowmax(s2);
+      const float mx = rowmax(s2) * c;
       const float m_old = m;
       if (trig) set_m(maxf(m_old, mx));
       const float alpha = m > m_old ? exp2_fast(m_old - m) : 1.f;  // 0 when m was -inf
       l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) acc[dt] *= alpha;
-      const float nm = m == -INFINITY ? 0.f : -m;
-      const float adj = (m_old == -INFINITY ? 0.f : m_old) + nm;  // 0 for rows that keep m
-#pragma unroll
-      for (int mt2 = 0; mt2 < C::MT; ++mt2) sx[mt2] += adj;
 #pragma unroll
       for (int e = 0; e < C::NE; e += 2) {
         const int m2 = e / 16, ee = e % 16;
         const uint32_t w = pq[2 * m2 + (ee >> 3)][(ee & 7) >> 1];
         pq[2 * m2 + (ee >> 3)][(ee & 7) >> 1] =
-            trig ? E::pack2(exp2_fast(s2[m2][ee] + nm), exp2_fast(s2[m2][ee + 1] + nm)) : w;
+            trig ? E::pack2(exp2_fast(fmaf(s2[m2][ee], c, nm)), exp2_fast(fmaf(s2[m2][ee + 1], c, nm))) : w;
       }
       f32x4 t2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -731,8 +673,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
     l += ts;
   };
 
-  // One pipeline step t: ST = t % NST, PV = t > 0. sc = S(t) - m, sn
-  // receives S(t+1) - m, pb receives P(t), pp holds P(t-1).
+  // One pipeline step t: ST = t % NST, PV = t > 0. sc = S(t), sn receives
+  // S(t+1), pb receives P(t), pp holds P(t-1).
   auto step = [&](auto ST, auto PV, const int t, f32x16* sc, f32x16* sn, u32x4* pb, u32x4* pp) CIE_INLINE {
     constexpr int st = decltype(ST)::value;
     constexpr int st1 = (st + 1) % C::NST, stp = (st + C::NST - 1) % C::NST;
@@ -760,7 +702,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
 #pragma unroll
     for (int i = 0; i < LA; ++i) fetch(i);
 #pragma unroll
-    for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = E::mfma(a_one, u32x4{bm, 0u, 0u, 0u}, f32x16{});
+    for (int mt2 = 0; mt2 < C::MT; ++mt2) sn[mt2] = f32x16{};
     f32x4 tsum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     // VALU chunk c: exp2 of scores [c EPC, (c + 1) EPC) of S(t) (score tile
     // e / 16, element e % 16), pairs packed into P(t); every four packed p
@@ -770,15 +712,15 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
 #pragma unroll
       for (int e = c0 * C::EPC; e < (c0 + 1) * C::EPC; ++e) {
         const int m2 = e / 16, ee = e % 16;
-        sc[m2][ee] = exp2_fast(sc[m2][ee]);
+        sc[m2][ee] = exp2_fast(fmaf(sc[m2][ee], c, nm));
         if (ee & 1) {
           const uint32_t pk = E::pack2(sc[m2][ee - 1], sc[m2][ee]);
           asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
           pb[2 * m2 + (ee >> 3)][(ee & 7) >> 1] = pk;
         }
         if ((ee & 3) == 3) {
-          const int c = 2 * m2 + (ee >> 3), w = (ee & 7) >> 1;
-          tsum[(ee >> 2) & 1] = E::mfma4(sum_ones, u32x2{pb[c][w - 1], pb[c][w]}, tsum[(ee >> 2) & 1]);
+          const int cb = 2 * m2 + (ee >> 3), w = (ee & 7) >> 1;
+          tsum[(ee >> 2) & 1] = E::mfma4(sum_ones, u32x2{pb[cb][w - 1], pb[cb][w]}, tsum[(ee >> 2) & 1]);
         }
       }
     };
@@ -799,7 +741,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
       __builtin_amdgcn_sched_barrier(0);
     });
     __builtin_amdgcn_s_setprio(0);
-    check(t, ring + st * C::STAGE, pb, sn, xhalf_sum(tsum[0][0] + tsum[1][0]));
+    check(t, ring + st * C::STAGE, pb, xhalf_sum(tsum[0][0] + tsum[1][0]));
     mask(t + 1, sn);
   };
 
@@ -860,7 +802,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_il_kernel(const FlashParams 
 // groups are the same 32 rows of two query heads that share the kv head
 // (128-row workgroups; a wave's causal span stays 32 rows); otherwise they
 // are rows q0w + 32 rg + l32 of one head (256-row workgroups). Per tile and
-// wave: 2 -m blocks + 8 QK^T MFMAs, 32 exp2 per lane, 8 P.V MFMAs. The
+// wave: 8 QK^T MFMAs, 32 fma + exp2 per lane, 8 P.V MFMAs. The
 // copies, causal rule and lazy max are those of flash_fwd_kernel; the slow
 // path acts on the rows that triggered it only (as in flash_fwd_il_kernel).
 template <int D, bool HEADS>
@@ -877,7 +819,7 @@ struct R64Cfg {
   static constexpr int NST = 4;                // ring stages (measured against 6 and 8: 2 % faster)
   static constexpr int NW = BN * S / 256;      // 1 KiB copies per wave per tensor
   static constexpr int PER_TILE = 2 * NW;
-  static constexpr int NQK = KK * NRG;         // QK^T MFMAs per tile (plus the -m blocks)
+  static constexpr int NQK = KK * NRG;         // QK^T MFMAs per tile
   static constexpr int EPC = 16 * NRG / NQK;   // S(t) elements per QK MFMA
   static_assert(D == 64, "two row groups per wave fit the registers at head_dim 64");
   static_assert(NW * 256 == BN * S, "tile must split evenly over 4 waves");
@@ -898,10 +840,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
   // divides evenly) and dispatches it longest first across all of its kv
   // heads: items are few and long here, and kv-head-major order left long
   // items for the end of the run.
-  const int N = p.n_wg;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int x0 = xcd * (N >> 3) + min(xcd, N & 7);           // first item of the run
-  const int cnt = (N >> 3) + (xcd < (N & 7) ? 1 : 0);         // items of the run (slot < cnt)
+  const int N = p.n_wg, xmask = (1 << p.xcd_shift) - 1;
+  const int xcd = blockIdx.x & xmask, slot = blockIdx.x >> p.xcd_shift;
+  const int x0 = xcd * (N >> p.xcd_shift) + min(xcd, N & xmask);    // first item of the run
+  const int cnt = (N >> p.xcd_shift) + (xcd < (N & xmask) ? 1 : 0);  // items of the run (slot < cnt)
   const int G = p.group, GI = HEADS ? G / 2 : G;
   const int per_grp = p.n_mt * GI;                            // items per kv head
   int grp, mt, g;
@@ -930,23 +872,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
     hq[rg] = HEADS ? kvh * G + 2 * g + rg : kvh * G + g;
   }
 
+  // q rows as loaded, sign flipped when the caller's scale is negative
   u32x4 qf[NRG][C::KK];
+  const float c = p.scale_log2;
+  const u32x4 qsg = {p.q_sign, p.q_sign, p.q_sign, p.q_sign};
   {
-    const float c = p.scale_log2;
-    const float cq = p.q_sign ? -c : c;
     if (!p.rope.cos) {
 #pragma unroll
       for (int rg = 0; rg < NRG; ++rg) {
         const uint16_t* qrow = p.q + b * p.qs0 + hq[rg] * p.qs1 + (int64_t)qi[rg] * p.qs2;
 #pragma unroll
-        for (int kk = 0; kk < C::KK; ++kk) qf[rg][kk] = load16(qrow + 16 * kk + 8 * hl, qi[rg] < p.Lq);
-#pragma unroll
-        for (int kk = 0; kk < C::KK; ++kk)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const f32x2 v = unpack2<DTYPE>(qf[rg][kk][w]);
-            qf[rg][kk][w] = E::pack2(v[0] * cq, v[1] * cq);
-          }
+        for (int kk = 0; kk < C::KK; ++kk) qf[rg][kk] = load16(qrow + 16 * kk + 8 * hl, qi[rg] < p.Lq) ^ qsg;
       }
     } else {
       // With RoPE every q load of the lane is issued first (rows clamped into
@@ -987,11 +923,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
         for (int kk = 0; kk < C::KK; ++kk) {
           if (!ok[r]) qf[rg][kk] = u32x4{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};  // outside the tables: NaN
           if (!live[rg]) qf[rg][kk] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const f32x2 v = unpack2<DTYPE>(qf[rg][kk][w]);
-            qf[rg][kk][w] = E::pack2(v[0] * cq, v[1] * cq);
-          }
+          qf[rg][kk] ^= qsg;
         }
       }
     }
@@ -1057,7 +989,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
     const int sl = (2 * kk + hl) ^ chunk_swizzle<C::S>(l32);
     return *reinterpret_cast<const u32x4*>(ks + (l32 * C::S + sl) * 8);
   };
-  // S^T of both row groups from the tile in stage ks (no -m block).
+  // S^T of both row groups from the tile in stage ks.
   auto qk = [&](const uint16_t* ks, f32x16* s) CIE_INLINE {
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) s[rg] = f32x16{};
@@ -1098,23 +1030,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
   for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) acc[rg][dt] = f32x16{};
-  float m[NRG], l[NRG];  // l: the row's sum over both lanes
-  uint32_t bm[NRG];      // word 0 of the -m block's B operand
-  constexpr float kMScale = DTYPE == 0 ? 256.f : 1.f;  // fp16 range for |m| up to 2^24
-  const u32x4 a_one = {hl == 0 ? E::pack2(kMScale, 0.f) : 0u, 0u, 0u, 0u};
-  auto set_m = [&](int rg, float x) CIE_INLINE {  // m = x rounded to what the B operand holds exactly
-    if (x != -INFINITY) {
-      x = fminf(x, 65504.f * kMScale);
-      x = unpack2<DTYPE>(E::pack2(x * (1.f / kMScale), 0.f))[0] * kMScale;
-    }
+  // m: a row's reference max in the exp2 domain (c * s); nm = -m, or 0
+  // while m is -inf. l: the row's sum over both lanes.
+  float m[NRG], l[NRG], nm[NRG];
+  auto set_m = [&](int rg, float x) CIE_INLINE {
     m[rg] = x;
-    bm[rg] = hl == 0 && x != -INFINITY ? E::pack2(-x * (1.f / kMScale), 0.f) : 0u;
+    nm[rg] = x == -INFINITY ? 0.f : -x;
   };
 #pragma unroll
   for (int rg = 0; rg < NRG; ++rg) {
-    m[rg] = -INFINITY;
+    set_m(rg, -INFINITY);
     l[rg] = 0.f;
-    bm[rg] = 0u;
   }
   // Row sums of P: 4x4x4 MFMAs with A all ones (see flash_fwd_kernel).
   const u32x2 sum_ones = {E::pack2(1.f, 1.f), E::pack2(1.f, 1.f)};
@@ -1130,14 +1056,11 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
     qk(ring, sc);
     mask(0, sc);
 #pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) {
-      set_m(rg, xhalf_max(max16(sc[rg])));  // the reference max starts at tile 0's row max
-      sc[rg] -= m[rg] == -INFINITY ? 0.f : m[rg];
-    }
+    for (int rg = 0; rg < NRG; ++rg) set_m(rg, xhalf_max(max16(sc[rg])) * c);  // the reference max starts at tile 0's row max
   }
 
-  // One pipeline step: sc holds S(t) - m, S(t+1) - m is produced in sn; ST is
-  // the ring stage of tile t.
+  // One pipeline step: sc holds S(t), S(t+1) is produced in sn; ST is the
+  // ring stage of tile t.
   auto step = [&](auto ST, const int t, f32x16* sc, f32x16* sn) CIE_INLINE {
     constexpr int st = decltype(ST)::value, st1 = (st + 1) % C::NST;
     if (t + 1 < n_tiles) {
@@ -1158,7 +1081,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
       for (int kk = 0; kk < C::KK; ++kk) ka[kk] = kfrag(ks, kk);
 #pragma unroll
       for (int rg = 0; rg < NRG; ++rg) {
-        sn[rg] = E::mfma(a_one, u32x4{bm[rg], 0u, 0u, 0u}, f32x16{});
+        sn[rg] = f32x16{};
         tsm[rg] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
@@ -1169,15 +1092,15 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
 #pragma unroll
         for (int e = i * C::EPC; e < (i + 1) * C::EPC; ++e) {
           const int rg = e / 16, ee = e % 16;
-          sc[rg][ee] = exp2_fast(sc[rg][ee]);
+          sc[rg][ee] = exp2_fast(fmaf(sc[rg][ee], c, nm[rg]));
           if (ee & 1) {
             const uint32_t pk = E::pack2(sc[rg][ee - 1], sc[rg][ee]);
             asm volatile("" ::"v"(pk));  // pin the work of this chunk next to its MFMA
             pb[rg][ee >> 3][(ee & 7) >> 1] = pk;
           }
           if ((ee & 3) == 3) {
-            const int c = ee >> 3, w = (ee & 7) >> 1;
-            tsm[rg] = E::mfma4(sum_ones, u32x2{pb[rg][c][w - 1], pb[rg][c][w]}, tsm[rg]);
+            const int cb = ee >> 3, w = (ee & 7) >> 1;
+            tsm[rg] = E::mfma4(sum_ones, u32x2{pb[rg][cb][w - 1], pb[rg][cb][w]}, tsm[rg]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1200,21 +1123,19 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
       mask(t, sc);
 #pragma unroll
       for (int rg = 0; rg < NRG; ++rg) {
-        const float mx = xhalf_max(max16(sc[rg]));
+        const float mx = xhalf_max(max16(sc[rg])) * c;
         const float m_old = m[rg];
         if (trig[rg]) set_m(rg, maxf(m_old, mx));
         const float alpha = m[rg] > m_old ? exp2_fast(m_old - m[rg]) : 1.f;  // 0 when m was -inf
         l[rg] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt) acc[rg][dt] *= alpha;
-        const float nm = m[rg] == -INFINITY ? 0.f : -m[rg];
-        const float adj = (m_old == -INFINITY ? 0.f : m_old) + nm;  // 0 for rows that keep m
-        sn[rg] += adj;
 #pragma unroll
         for (int e = 0; e < 16; e += 2) {
           const uint32_t w = pb[rg][e >> 3][(e & 7) >> 1];
           pb[rg][e >> 3][(e & 7) >> 1] =
-              trig[rg] ? E::pack2(exp2_fast(sc[rg][e] + nm), exp2_fast(sc[rg][e + 1] + nm)) : w;
+              trig[rg] ? E::pack2(exp2_fast(fmaf(sc[rg][e], c, nm[rg])), exp2_fast(fmaf(sc[rg][e + 1], c, nm[rg])))
+                       : w;
         }
         f32x4 t2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1288,7 +1209,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
 //
 // A two-row-group item is twice the work of a flash_fwd_kernel item and there
 // are half as many, so it pays only with enough of them: at least one per
-// workgroup slot of the GPU (256 CUs x 2), and, causal, its longest item
+// workgroup slot of the GPU (2 per CU: 512 on an MI355X), and, causal, its longest item
 // (the last query tile: every key, 32 per step, plus ~4 steps of start-up)
 // within 1.6x the average work per slot; otherwise the critical path or the
 // idle slots cost more than the shared fragment reads save (measured on
@@ -1299,7 +1220,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
 // size, so GQA and its expanded MHA take the same kernel and stay equal bit
 // for bit.
 static bool r64_pays(const FlashParams& p) {
-  constexpr int64_t kSlots = 2 * kPagedCUs, kStartup = 4;
+  const int64_t kSlots = 2 * (int64_t)p.cus, kStartup = 4;
   if (p.Lq <= 128) return false;
   const int64_t n_mt = (p.Lq + 127) / 128;
   const int64_t items = (int64_t)(p.n_wg / p.n_mt) / 2;  // B * Hq / 2 per query tile
@@ -1323,16 +1244,27 @@ static void launch_r64(const FlashParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((flash_fwd_r64_kernel<DTYPE, D, HEADS>), dim3(q.n_wg), dim3(256), 0, stream, q);
 }
 
+FlashKernel flash_kernel_choice(const FlashParams& p, int D) {
+  if (D == 128) return kFlashIl;
+  if (D == 64 && r64_pays(p)) return p.group % 2 == 0 ? kFlashR64Heads : kFlashR64Rows;
+  return kFlash32;
+}
+
 template <int DTYPE, int D>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t stream) {
-  if constexpr (D == 128) {
-    hipLaunchKernelGGL((flash_fwd_il_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
-  } else if constexpr (D == 64) {
-    if (!r64_pays(p)) hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
-    else if (p.group % 2 == 0) launch_r64<DTYPE, D, true>(p, stream);
-    else launch_r64<DTYPE, D, false>(p, stream);
-  } else {
-    hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+  switch (flash_kernel_choice(p, D)) {
+    case kFlashIl:
+      if constexpr (D == 128) hipLaunchKernelGGL((flash_fwd_il_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+      break;
+    case kFlashR64Heads:
+      if constexpr (D == 64) launch_r64<DTYPE, D, true>(p, stream);
+      break;
+    case kFlashR64Rows:
+      if constexpr (D == 64) launch_r64<DTYPE, D, false>(p, stream);
+      break;
+    default:
+      if constexpr (D != 128) hipLaunchKernelGGL((flash_fwd_kernel<DTYPE, D>), dim3(p.n_wg), dim3(256), 0, stream, p);
+      break;
   }
   return hipGetLastError();
 }

@@ -68,7 +68,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kI8BN = 128;  // weight rows per workgroup
 constexpr int kI8BK = 64;   // k per step
-constexpr int kI8MaxSplitTiles = 256;  // K is split only when there are fewer (n, m) tiles
 
 constexpr int kI8MaxSplits = 16;
 
@@ -203,9 +202,7 @@ __global__ __launch_bounds__(256 * KW, KW == 1 ? 2 : 1) void int8_gemm_kernel(co
   // tile order: the m tiles of one weight tile are consecutive logical ids,
   // and consecutive logical ids land on one XCD (round-robin dispatch), so a
   // weight tile read by several m tiles is shared through that XCD's L2
-  const int NWG = p.n_tiles * p.m_tiles * p.splits;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int logical = xcd * (NWG >> 3) + min(xcd, NWG & 7) + slot;
+  const int logical = xcd_logical(blockIdx.x, p.n_tiles * p.m_tiles * p.splits, p.xcd_shift);
   const int split = logical % p.splits;
   const int rest = logical / p.splits;
   const int mt_i = rest % p.m_tiles;
@@ -728,8 +725,9 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
   }
 }
 
-I8Geom int8_gemm_geometry(int M, int N, int K) {
+I8Geom int8_gemm_geometry(int M, int N, int K, DeviceShape dev) {
   I8Geom g{};
+  g.dev = dev;
   g.n_tiles = (N + kI8BN - 1) / kI8BN;
   g.ksteps = K / kI8BK;
   if (M <= 64) {  // weight streaming, one launch, no workspace (2: VALU dot products)
@@ -745,8 +743,9 @@ I8Geom int8_gemm_geometry(int M, int N, int K) {
   // per CU; failing both, 128 rows when that gives one tile per CU, else 64
   // (N = K = 4096: M = 1024 ran 47.3 us at 64 rows against 52.1 at 128; at
   // M = 512, 32-row tiles or a K split for two tiles per CU were slower)
+  const int64_t cus = dev.cus;
   const int64_t t128 = (int64_t)g.n_tiles * ((M + 127) / 128), t64 = (int64_t)g.n_tiles * ((M + 63) / 64);
-  g.mt = t128 >= 512 ? 4 : (t64 >= 512 ? 2 : (t128 >= 256 ? 4 : 2));
+  g.mt = t128 >= 2 * cus ? 4 : (t64 >= 2 * cus ? 2 : (t128 >= cus ? 4 : 2));
   // 3-4 ring stages let two workgroups share a CU
   g.nst = g.mt >= 4 ? 3 : 4;
   const int bm = 32 * g.mt;
@@ -754,8 +753,13 @@ I8Geom int8_gemm_geometry(int M, int N, int K) {
   const int64_t tiles = (int64_t)g.m_tiles * g.n_tiles;
   // split K only as far as needed for one workgroup per CU, keeping >= 4 k steps per split
   int s = 1;
-  if (tiles < kI8MaxSplitTiles) s = (int)std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, g.ksteps / 4));
+  if (tiles < cus) s = (int)std::min<int64_t>((cus + tiles - 1) / tiles, std::max(1, g.ksteps / 4));
   g.splits = std::max(1, std::min(s, kI8MaxSplits));
+  // one workgroup per CU or fewer: eight waves (two k halves) so every SIMD
+  // holds two waves (512 x 4096 x 4096: 31.9 -> 30.1 us); else four waves and
+  // two workgroups per CU. Not with K split three ways or more (128 x 4096 x
+  // 4096, four splits: 1 % slower).
+  g.kw2 = tiles * g.splits <= cus && g.splits <= 2;
   g.m_pad = g.m_tiles * bm;
   g.n_pad = g.n_tiles * kI8BN;
   g.workspace_bytes = g.splits > 1 ? (size_t)g.splits * g.m_pad * g.n_pad * sizeof(float) : 0;
@@ -764,15 +768,10 @@ I8Geom int8_gemm_geometry(int M, int N, int K) {
 }
 
 template <int DTYPE, int MT, int NST>
-static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, hipStream_t stream) {
+static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, bool kw2, hipStream_t stream) {
   using C = I8Cfg<MT, NST>;
   if (lds != (size_t)C::NST * C::STAGE) return hipErrorInvalidValue;  // geometry and kernel disagree
   const int nwg = p.n_tiles * p.m_tiles * p.splits;
-  // one workgroup per CU or fewer: eight waves (two k halves) so every SIMD
-  // holds two waves (512 x 4096 x 4096: 31.9 -> 30.1 us); else four waves and
-  // two workgroups per CU. Not with K split three ways or more (128 x 4096 x
-  // 4096, four splits: 1 % slower).
-  const bool kw2 = nwg <= kPagedCUs && p.splits <= 2;
   const void* fn = kw2 ? reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST, 2>)
                        : reinterpret_cast<const void*>(&int8_gemm_kernel<DTYPE, MT, NST, 1>);
   const hipError_t attr = set_dynamic_lds(fn, C::NST * C::STAGE);
@@ -802,8 +801,8 @@ static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_
     if (p.M <= 32) return launch_ws_t<DTYPE, 32, 1, 2>(p, stream);
     return launch_ws_t<DTYPE, 64, 2, 4>(p, stream);
   }
-  if (g.mt == 2 && g.nst == 4) return launch_i8_t<DTYPE, 2, 4>(p, g.lds_bytes, stream);
-  if (g.mt == 4 && g.nst == 3) return launch_i8_t<DTYPE, 4, 3>(p, g.lds_bytes, stream);
+  if (g.mt == 2 && g.nst == 4) return launch_i8_t<DTYPE, 2, 4>(p, g.lds_bytes, g.kw2, stream);
+  if (g.mt == 4 && g.nst == 3) return launch_i8_t<DTYPE, 4, 3>(p, g.lds_bytes, g.kw2, stream);
   return hipErrorInvalidValue;
 }
 

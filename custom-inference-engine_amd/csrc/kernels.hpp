@@ -10,6 +10,21 @@
 
 namespace cie {
 
+// The GPU a launch is sized for: its compute units, and its XCDs (2^xcd_shift
+// of them), over which workgroup ids are dispatched round-robin, each XCD
+// with its own L2. On gfx950 an XCD has 32 active CUs: 8 XCDs and 256 CUs as
+// one partition (an MI355X), fewer when the GPU is partitioned.
+struct DeviceShape {
+  int cus;
+  int xcd_shift;
+};
+constexpr int kDefaultCUs = 256;  // an unpartitioned MI355X
+DeviceShape shape_for_cus(int cus);
+// The current device's shape, queried once per device; the MI355X's when no
+// device can be queried (size and argument checks on a host without a GPU).
+// Thread-safe.
+DeviceShape device_shape();
+
 // Rotary tables of the kernels that apply RoPE: cos, sin of shape (rows, D/2),
 // contiguous, elements of type dt (kTabF16, kTabBF16 or kTabF32).
 // cos == nullptr: no rotation.
@@ -39,7 +54,13 @@ struct FlashParams {
   int causal;
   RopeTables rope;        // rotate q rows as they are loaded: row i of batch b at position q_pos0[b] + i
   const int32_t* q_pos0;  // [B] or nullptr (position = row)
+  int cus;                // compute units of the device (kernel choice)
+  int xcd_shift;          // log2 of its XCDs (workgroup placement)
 };
+
+// Prefill kernel a launch takes (launch_flash); cie_prefill_kernel reports it.
+enum FlashKernel { kFlash32 = 0, kFlashR64Heads = 1, kFlashR64Rows = 2, kFlashIl = 3 };
+FlashKernel flash_kernel_choice(const FlashParams& p, int D);
 
 // Paged attention over a (num_blocks, block_size, Hk, D) pool.
 //
@@ -69,6 +90,7 @@ struct PagedParams {
   FastDiv bsdiv;
   FastDiv rtdiv, nwvdiv, ngdiv;  // item decomposition of the merge pass
   int xcd_runs;   // ranges of a head group in contiguous runs per XCD (paged_xcd_runs)
+  int xcd_shift;  // log2 of the device's XCDs
   int mtab_cap;   // > 0: the merge pass takes its sequences from the plan's merge table (capacity per XCD)
   int plan_mtab;  // offset of that table in the plan (int32 elements)
   int Hg, NG, n_qt, NWV, NCH, NST, Wg;
@@ -87,6 +109,7 @@ struct PagedParams {
   // derived on the device from lens and bt. Offsets in int32 elements.
   const int32_t* plan;
   int plan_ranges, plan_entries, plan_ids, plan_empty;
+  int plan_split;  // split sequences the caller says the plan has (checked against its header)
 };
 
 constexpr int kPagedTile = 32;         // tokens per tile
@@ -98,7 +121,6 @@ constexpr int kPagedMaxWaves = 8;      // waves per workgroup (head_dim 256: pag
 // share a SIMD, so those workgroups have at most four waves (one per SIMD)
 // and at most 128 query rows per kv head.
 __host__ __device__ constexpr int paged_max_waves(int D) { return D == 256 ? 4 : kPagedMaxWaves; }
-constexpr int kPagedCUs = 256;         // compute units the launch is sized for
 constexpr int kPagedLdsBudget = 150 * 1024;
 
 // Launch geometry of a paged call; a pure function of the arguments, so the
@@ -106,6 +128,8 @@ constexpr int kPagedLdsBudget = 150 * 1024;
 struct PagedGeom {
   int ok;            // 0: shape not supported (error text in err)
   const char* err;
+  int Hq, D;         // the shape's query heads and head_dim
+  DeviceShape dev;   // the GPU the launch is sized for
   int R, Rt, n_qt;
   int Hg, NG, NWV;   // kv heads per workgroup, head groups, waves per workgroup
   int NCH;           // 16-byte chunks per token row of a head group (Hg * D / 8)
@@ -114,39 +138,63 @@ struct PagedGeom {
   size_t lds_bytes;  // dynamic LDS per workgroup
   size_t info_bytes, slot_bytes;  // workspace parts
 };
-PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size);
+PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size, DeviceShape dev);
 
 // Host-built plan of a paged launch (see paged_plan.cpp for the layout).
-constexpr int32_t kPlanMagic = 0x43504c31;  // "CPL1"
+constexpr int32_t kPlanMagic = 0x43504c32;  // "CPL2"
 constexpr int kPlanHeader = 16;             // header ints
+// Header fields (int32 indices): every argument the plan's layout, ranges
+// and validated block ids depend on, compared by the launch before it reads
+// anything else of the plan.
+enum PlanHeader {
+  kPlMagic = 0, kPlW = 1, kPlNT = 2, kPlWg = 3, kPlEmpty = 4, kPlSplit = 5, kPlB = 6, kPlAppend = 7,
+  kPlNG = 8, kPlLq = 9, kPlD = 10, kPlNumBlocks = 11, kPlBlockSize = 12, kPlMaxBlocks = 13, kPlCtxLimit = 14,
+  kPlHq = 15
+};
 constexpr int kPlanRangeInts = 8;           // ints per range row
 struct PlanLayout {
   size_t ranges, entries, ids, info, empty, mtab;  // section offsets (int32 elements)
   size_t ints;                                     // total size
 };
 // The main pass places the ranges of a head group on the XCDs in contiguous
-// runs (workgroup ids are dispatched round-robin over the 8 XCDs, and each
-// XCD keeps what its workgroups wrote in its L2 across the kernel boundary),
-// and the plan's merge table hands each split sequence's merge work to the
-// XCD holding its pieces: mtab[x][i] (x < 8, i < merge_table_cap(B, NG)) is
-// the i-th sequence (b * NG + gh) merged on XCD x, -1 when unused.
-// Sequences per XCD list: every split sequence fits, with one to spare.
-__host__ __device__ inline int merge_cap(int split_units) { return (split_units + 7) / 8 + 1; }
-__host__ __device__ inline int merge_table_cap(int B, int NG) { return merge_cap(B * NG); }
+// runs (workgroup ids are dispatched round-robin over the XCDs, and each XCD
+// keeps what its workgroups wrote in its L2 across the kernel boundary), and
+// the plan's merge table hands each split sequence's merge work to the XCD
+// holding its pieces: mtab[x][i] (x < kMaxXcds, i < merge_table_cap(...)) is
+// the i-th sequence (b * NG + gh) merged on XCD x, -1 when unused (lists of
+// XCDs the device does not have stay empty).
+constexpr int kMaxXcds = 8;
+// Sequences per XCD list over 2^xcd_shift XCDs: every split sequence fits,
+// with one to spare.
+__host__ __device__ inline int merge_cap(int split_units, int xcd_shift) {
+  return ((split_units + (1 << xcd_shift) - 1) >> xcd_shift) + 1;
+}
+__host__ __device__ inline int merge_table_cap(int B, int NG, int xcd_shift) { return merge_cap(B * NG, xcd_shift); }
 // The placement (and the merge table) is used when the main pass has one
 // workgroup per CU or fewer (verify-like shapes: partial states of ~20 query
 // rows per kv head, merge reads from L2 3.8 % faster on verify_b8); with two
 // workgroups per CU (decode-like) contiguous runs cost the main pass more
 // than the merge saves (decode_b32 +1.2 us), and ranges alternate head
 // groups over the workgroup ids instead.
-inline bool paged_xcd_runs(int NG, int Wg) { return (int64_t)NG * Wg <= 256; }
-// XCD of main-pass workgroup `logical` (the order of the remap below) when
-// the grid has n workgroups.
-inline int xcd_of_logical(int64_t logical, int64_t n) {
-  const int64_t base = n >> 3, extra = n & 7;
-  for (int x = 0; x < 7; ++x)
+inline bool paged_xcd_runs(const PagedGeom& g) { return (int64_t)g.NG * g.Wg <= g.dev.cus; }
+// XCD of main-pass workgroup `logical` (the order of xcd_logical) when the
+// grid has n workgroups over 2^xcd_shift XCDs.
+inline int xcd_of_logical(int64_t logical, int64_t n, int xcd_shift) {
+  const int nx = 1 << xcd_shift;
+  const int64_t base = n >> xcd_shift, extra = n & (nx - 1);
+  for (int x = 0; x < nx - 1; ++x)
     if (logical < (x + 1) * base + std::min<int64_t>(x + 1, extra)) return x;
-  return 7;
+  return nx - 1;
+}
+
+// Workgroup `block` of an n-workgroup grid, renumbered so that each XCD
+// (block % 2^xcd_shift, the round-robin dispatch) holds a contiguous run of
+// logical ids: XCD x takes ids [start_x, start_x + count_x), the counts in
+// XCD order. A bijection of [0, n) for every n.
+__device__ __forceinline__ int xcd_logical(int block, int n, int xcd_shift) {
+  const int mask = (1 << xcd_shift) - 1;
+  const int xcd = block & mask, slot = block >> xcd_shift;
+  return xcd * (n >> xcd_shift) + min(xcd, n & mask) + slot;
 }
 PlanLayout paged_plan_layout(const PagedGeom& g, int B, int max_blocks);
 // Fills P (layout L) from host lengths and block tables; returns the number
@@ -213,19 +261,22 @@ struct I8GemmParams {
   int64_t xs, wsr, ys;
   int M, N, K, scale_dtype;
   int n_tiles, m_tiles, splits, ksteps, m_pad, n_pad;
+  int xcd_shift;          // log2 of the device's XCDs
 };
 
 // Launch geometry of an INT8 GEMM; a pure function of (M, N, K), so the
 // workspace query and the launch agree.
 struct I8Geom {
   int gemv;                // 1: weight-streaming MFMA kernel (M <= 64), 2: VALU dot kernel (M = 1); one launch
+  int kw2;                 // tiled kernel: two K-waves per workgroup (eight waves)
+  DeviceShape dev;         // the GPU the launch is sized for
   int mt;                  // 32-row activation tiles per workgroup
   int nst;                 // LDS ring stages
   int m_tiles, n_tiles, ksteps, splits, m_pad, n_pad;
   size_t workspace_bytes;  // split-K partials (0 when splits == 1)
   size_t lds_bytes;
 };
-I8Geom int8_gemm_geometry(int M, int N, int K);
+I8Geom int8_gemm_geometry(int M, int N, int K, DeviceShape dev);
 
 // Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
 // per (kernel, device): the attribute is a property of the kernel as loaded

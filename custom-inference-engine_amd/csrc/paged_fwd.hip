@@ -92,11 +92,17 @@ __device__ __forceinline__ int div_small(uint64_t n, uint32_t d) {
   return n <= 0xffffffffull ? (int)((uint32_t)n / d) : (int)(n / d);
 }
 
-// The plan header names this launch: magic, range count, batch and whether
-// it was built for the fused append.
+// The plan header names the launch it was built for: every argument its
+// layout, ranges and validated block ids depend on, and the split count the
+// caller passes with it. Anything else of the plan is read only after this
+// check (one scalar load of the 16 header ints).
+template <int D>
 __device__ __forceinline__ bool plan_matches(const PagedParams& p) {
   const int32_t* P = p.plan;
-  return P[0] == kPlanMagic && P[3] == p.Wg && P[6] == p.B && P[7] == (p.kn ? 1 : 0);
+  return P[kPlMagic] == kPlanMagic && P[kPlWg] == p.Wg && P[kPlB] == p.B && P[kPlAppend] == (p.kn ? 1 : 0) &&
+         P[kPlSplit] == p.plan_split && P[kPlNG] == p.NG && P[kPlLq] == p.Lq && P[kPlD] == D &&
+         P[kPlNumBlocks] == p.num_blocks && P[kPlBlockSize] == p.block_size && P[kPlMaxBlocks] == p.max_blocks &&
+         P[kPlCtxLimit] == p.ctx_limit && P[kPlHq] == p.Hq;
 }
 
 __device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
@@ -164,14 +170,12 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
 
   // Range j of head group gh. With xcd_runs the ranges of a head group go to
   // the XCDs in contiguous runs (workgroups are dispatched round-robin over
-  // the 8 XCDs), so the pieces of a split sequence are mostly written through
+  // the XCDs), so the pieces of a split sequence are mostly written through
   // one XCD's L2, where the merge pass then finds them (merge_table_cap);
   // otherwise consecutive workgroup ids alternate head groups.
   int gh, j;
   if (p.xcd_runs) {
-    const int nwg = p.NG * p.Wg;
-    const int xcd = blockIdx.x & 7, xslot = blockIdx.x >> 3;
-    const int logical = xcd * (nwg >> 3) + min(xcd, nwg & 7) + xslot;
+    const int logical = xcd_logical(blockIdx.x, p.NG * p.Wg, p.xcd_shift);
     gh = logical / p.Wg;
     j = logical - gh * p.Wg;
   } else {
@@ -198,7 +202,7 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
     // ---- schedule from the host-built plan: this range's row, then its
     // entries and block ids (already validated) copied straight into LDS ----
     const int32_t* P = p.plan;
-    const bool ok = plan_matches(p);
+    const bool ok = plan_matches<D>(p);
     const int32_t* row = P + p.plan_ranges + kPlanRangeInts * j;
     if (ok) {
       ne = min(row[1], kPagedEntries);
@@ -756,16 +760,17 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   // merge table, workgroup (XCD x, slot s) takes part s % wpu of the x-th
   // list's sequence s / wpu; otherwise the sequences follow the grid.
   uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  // a plan built for other arguments: the main pass has written NaN rows,
+  // and the offsets of its descriptors and merge table may lie past its end
+  if (p.plan && !plan_matches<D>(p)) return;
   int unit = -1;
   if (p.mtab_cap > 0) {
-    // a plan built for other arguments: the main pass has written NaN rows,
-    // and the table's offset may lie past that plan's end
-    if (!plan_matches(p)) return;
     const uint32_t per_unit = (uint32_t)p.NWV * p.Rt * Q4 * kMergeLanes;
     const uint32_t wpu = (per_unit + 255) / 256;
-    const uint32_t slot = blockIdx.x >> 3, ui = slot / wpu;
+    const uint32_t slot = blockIdx.x >> p.xcd_shift, ui = slot / wpu;
+    const int xcd = (int)(blockIdx.x & ((1u << p.xcd_shift) - 1));
     if (ui < (uint32_t)p.mtab_cap)
-      unit = p.plan[p.plan_mtab + (int64_t)(blockIdx.x & 7) * merge_table_cap(p.B, p.NG) + ui];
+      unit = p.plan[p.plan_mtab + (int64_t)xcd * merge_table_cap(p.B, p.NG, p.xcd_shift) + ui];
     if (unit < 0 || unit >= p.B * p.NG) return;  // an unused (or invalid) entry: the whole workgroup idles
     tid = (slot - ui * wpu) * 256u + threadIdx.x;
   }
@@ -797,9 +802,8 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   const int pieces = inf.y;
   const int hh = w % p.Hg, qt = w / p.Hg;
   const int r = qt * 32 + row;
-  // a descriptor that does not name ranges of this launch (a plan built for
-  // other arguments) is ignored: the main pass has written NaN rows then
-  const bool described = inf.x >= 0 && pieces <= p.Wg && inf.x <= p.Wg - pieces && (!p.plan || plan_matches(p));
+  // a descriptor that does not name ranges of this launch is ignored
+  const bool described = inf.x >= 0 && pieces <= p.Wg && inf.x <= p.Wg - pieces;
   const bool act = in && pieces > 1 && r < p.R && described;
   const int64_t slot_floats = (int64_t)p.Rt * (D + 2);
 
@@ -833,9 +837,12 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   *reinterpret_cast<u32x2*>(orow + 4 * d4) = u32x2{E::pack2(A.x * inv, A.y * inv), E::pack2(A.z * inv, A.w * inv)};
 }
 
-PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size) {
+PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size, DeviceShape dev) {
   PagedGeom g{};
   g.ok = 0;
+  g.Hq = Hq;
+  g.D = D;
+  g.dev = dev;
   if (B < 1 || Hq < 1 || Hk < 1 || Lq < 1 || Hq % Hk || block_size < 1 || ctx_limit < 0 ||
       !(D == 16 || D == 32 || D == 64 || D == 128 || D == 256)) {
     g.err = "invalid shape";
@@ -873,7 +880,7 @@ PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, in
   const int64_t nt_upper = (int64_t)B * ((ctx_limit + kPagedTile - 1) / kPagedTile);
   const int ids_per_tile = (kPagedTile + block_size - 1) / block_size + 2;
   const int tcap = std::min(kPagedEntries, kPagedIds / ids_per_tile);
-  int64_t wg = std::max<int64_t>(1, (int64_t)kPagedCUs * wpc / g.NG);
+  int64_t wg = std::max<int64_t>(1, (int64_t)dev.cus * wpc / g.NG);
   wg = std::min<int64_t>(wg, std::max<int64_t>(1, nt_upper));
   wg = std::max<int64_t>(wg, (nt_upper + tcap - 1) / tcap);
   if (wg * g.NG > INT_MAX) {
@@ -905,7 +912,7 @@ static hipError_t launch_paged_t(const PagedParams& p, size_t lds, bool merge, h
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !merge) return e;
   const int64_t per_unit = (int64_t)p.NWV * p.Rt * (D / 4) * kMergeLanes;
-  const int64_t n_merge = p.mtab_cap > 0 ? (int64_t)8 * p.mtab_cap * ((per_unit + 255) / 256)
+  const int64_t n_merge = p.mtab_cap > 0 ? ((int64_t)p.mtab_cap << p.xcd_shift) * ((per_unit + 255) / 256)
                                          : ((int64_t)p.B * p.NG * per_unit + 255) / 256;
   hipLaunchKernelGGL((paged_merge_kernel<DTYPE, D>), dim3((unsigned)n_merge), dim3(256), 0, stream, p);
   return hipGetLastError();

@@ -18,8 +18,11 @@
 //
 // Layout (int32), offsets fixed by the launch geometry so the launch knows
 // them without reading the plan:
-//   header   kPlanHeader ints: magic, W, NT, Wg, empties, split sequences,
-//            B, append flag
+//   header   kPlanHeader ints (PlanHeader): magic, W, NT, Wg, empties,
+//            split sequences, B, append flag, then the arguments the layout
+//            and the validated ids depend on: NG, Lq, D, num_blocks,
+//            block_size, max_blocks, ctx_limit, Hq. A launch compares them
+//            all with its own before it reads anything else of the plan.
 //   ranges   Wg rows of kPlanRangeInts: first entry, entries, first id, ids,
 //            S0 (first tile), T (tiles)
 //   entries  (Wg + B) rows of 8: b, ctx, tt_lo, n, idb (from the range's
@@ -30,8 +33,9 @@
 //            merge pass's piece descriptors), zero for unsplit sequences
 //   empty    B rows of 2: sequences without tiles (b, 1 if the history is
 //            empty, 0 if its length is invalid)
-//   mtab     8 lists of merge_table_cap(B, NG): the split sequences
-//            (b * NG + gh) whose merge runs on each XCD, -1 past the end;
+//   mtab     kMaxXcds lists of merge_table_cap(B, NG, xcd_shift): the split
+//            sequences (b * NG + gh) whose merge runs on each XCD, -1 past
+//            the end (and in the lists of XCDs the device does not have);
 //            each goes to the XCD that ran its middle piece (its partial
 //            states are in that XCD's L2), or, when that list holds
 //            merge_cap(split sequences) already, to the shortest list
@@ -52,7 +56,7 @@ PlanLayout paged_plan_layout(const PagedGeom& g, int B, int max_blocks) {
   L.info = (L.info + 3) / 4 * 4;  // int4 aligned
   L.empty = L.info + (size_t)4 * g.NG * B;
   L.mtab = L.empty + (size_t)2 * B;
-  L.ints = L.mtab + (size_t)8 * merge_table_cap(B, g.NG);
+  L.ints = L.mtab + (size_t)kMaxXcds * merge_table_cap(B, g.NG, g.dev.xcd_shift);
   return L;
 }
 
@@ -142,34 +146,42 @@ int build_paged_plan(int32_t* P, const PagedGeom& g, const PlanLayout& L, const 
     ne_total += ne;
     nid_total += nid;
   }
-  (void)max_blocks;
   // merge table (launches placed in XCD runs only): every split sequence of
   // every head group, on the XCD of its middle piece when that list has room
   {
-    const int cap_t = merge_table_cap(B, g.NG), cap = merge_cap(split * g.NG);
+    const int xs = g.dev.xcd_shift, nx = 1 << xs;
+    const int cap_t = merge_table_cap(B, g.NG, xs), cap = merge_cap(split * g.NG, xs);
     int32_t* T = P + L.mtab;
-    for (int i = 0; i < 8 * cap_t; ++i) T[i] = -1;
-    if (paged_xcd_runs(g.NG, g.Wg)) {
-    int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int64_t n = (int64_t)g.NG * g.Wg;
-    for (int b = 0; b < B; ++b)
-      for (int gh = 0; gh < g.NG; ++gh) {
-        const int32_t* f = F + (size_t)4 * ((size_t)gh * B + b);
-        if (tiles[b] == 0 || f[1] <= 1) continue;
-        int x = xcd_of_logical((int64_t)gh * g.Wg + f[0] + f[1] / 2, n);
-        if (cnt[x] >= cap) x = (int)(std::min_element(cnt, cnt + 8) - cnt);
-        T[x * cap_t + cnt[x]++] = b * g.NG + gh;
-      }
+    for (int i = 0; i < kMaxXcds * cap_t; ++i) T[i] = -1;
+    if (paged_xcd_runs(g)) {
+      int cnt[kMaxXcds] = {0, 0, 0, 0, 0, 0, 0, 0};
+      const int64_t n = (int64_t)g.NG * g.Wg;
+      for (int b = 0; b < B; ++b)
+        for (int gh = 0; gh < g.NG; ++gh) {
+          const int32_t* f = F + (size_t)4 * ((size_t)gh * B + b);
+          if (tiles[b] == 0 || f[1] <= 1) continue;
+          int x = xcd_of_logical((int64_t)gh * g.Wg + f[0] + f[1] / 2, n, xs);
+          if (cnt[x] >= cap) x = (int)(std::min_element(cnt, cnt + nx) - cnt);
+          T[x * cap_t + cnt[x]++] = b * g.NG + gh;
+        }
     }
   }
-  P[0] = kPlanMagic;
-  P[1] = (int32_t)W;
-  P[2] = (int32_t)NT;
-  P[3] = g.Wg;
-  P[4] = n_empty;
-  P[5] = split;
-  P[6] = B;
-  P[7] = append ? 1 : 0;
+  P[kPlMagic] = kPlanMagic;
+  P[kPlW] = (int32_t)W;
+  P[kPlNT] = (int32_t)NT;
+  P[kPlWg] = g.Wg;
+  P[kPlEmpty] = n_empty;
+  P[kPlSplit] = split;
+  P[kPlB] = B;
+  P[kPlAppend] = append ? 1 : 0;
+  P[kPlNG] = g.NG;
+  P[kPlLq] = Lq;
+  P[kPlD] = g.D;
+  P[kPlNumBlocks] = num_blocks;
+  P[kPlBlockSize] = block_size;
+  P[kPlMaxBlocks] = max_blocks;
+  P[kPlCtxLimit] = ctx_limit;
+  P[kPlHq] = g.Hq;
   return split;
 }
 

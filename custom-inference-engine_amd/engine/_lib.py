@@ -16,7 +16,7 @@ import torch
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("CIE_ATTN_LIB", os.path.join(PKG_ROOT, "libcie_attn.so"))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CIE_OK = 0
 CIE_EINVAL = -1
@@ -31,6 +31,8 @@ TABLE_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 EXPORTED_SYMBOLS = (
     "cie_abi_version",
     "cie_last_error",
+    "cie_device_cus",
+    "cie_prefill_kernel",
     "cie_flash_fwd",
     "cie_paged_workspace_bytes",
     "cie_paged_fwd",
@@ -67,6 +69,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cie_abi_version.restype = _i
     lib.cie_last_error.argtypes = []
     lib.cie_last_error.restype = ctypes.c_char_p
+    lib.cie_device_cus.argtypes = []
+    lib.cie_device_cus.restype = _i
+    lib.cie_prefill_kernel.argtypes = [_i, _i, _i, _i, _i, _i, _i, _i, _i]
+    lib.cie_prefill_kernel.restype = _i
     lib.cie_flash_fwd.argtypes = [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
                                   _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i, _vp]
     lib.cie_flash_fwd.restype = _i

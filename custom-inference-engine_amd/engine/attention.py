@@ -154,6 +154,38 @@ def flash_attention(
     return out
 
 
+_PREFILL_KERNELS = {0: "flash_fwd", 1: "r64_heads", 2: "r64_rows", 3: "il"}
+
+
+def prefill_kernel(B: int, Hq: int, Hk: int, Lq: int, Lk: int, D: int, causal: bool = True,
+                   dtype: torch.dtype = torch.float16, cu_count: int = 0) -> str:
+    """Name of the prefill kernel :func:`flash_attention` runs for this shape
+    (``cie_prefill_kernel``): ``"flash_fwd"`` (32 query rows per wave),
+    ``"r64_heads"`` / ``"r64_rows"`` (head_dim 64, two 32-row groups per
+    wave: the same rows of two query heads, or 64 rows of one head) or
+    ``"il"`` (head_dim 128, interleaved MFMA / softmax stream). ``cu_count``:
+    compute units to size for, 0 for the current device."""
+    rc = _lib.load().cie_prefill_kernel(B, Hq, Hk, Lq, Lk, D, 1 if causal else 0, _lib.DTYPE_CODES[dtype],
+                                        int(cu_count))
+    if rc < 0:
+        _lib.check(rc)
+    return _PREFILL_KERNELS[rc]
+
+
+def device_cus() -> int:
+    """Compute units of the current device, as the library sizes its
+    launches for it (``cie_device_cus``)."""
+    return int(_lib.load().cie_device_cus())
+
+
+def _plan_fingerprint(context_lens: torch.Tensor, block_tables: torch.Tensor) -> int:
+    """A cheap hash of host lengths and block-table rows (the bytes a plan is
+    built from)."""
+    import zlib
+
+    return zlib.crc32(block_tables.numpy().tobytes(), zlib.crc32(context_lens.numpy().tobytes()))
+
+
 @dataclass(frozen=True)
 class PagedPlan:
     """A host-built work plan of paged attention (``cie_paged_plan``): the
@@ -161,10 +193,21 @@ class PagedPlan:
     descriptors of the merge pass, for one launch shape and one set of
     context lengths and block tables. ``data`` is the int32 plan (on the
     device for a launch), ``split`` the number of sequences split across
-    workgroups, ``key`` the launch shape it was built for."""
+    workgroups, ``key`` the launch shape it was built for, ``fingerprint``
+    a hash of the host lengths and block tables it was built from (see
+    :meth:`built_from`)."""
     data: torch.Tensor
     split: int
     key: tuple
+    fingerprint: int = 0
+
+    def built_from(self, context_lens: torch.Tensor, block_tables: torch.Tensor) -> bool:
+        """Whether the plan was built from these host lengths and tables (a
+        launch with a plan reads neither: a plan of an earlier step with the
+        same shape would attend over that step's lengths and blocks)."""
+        lens = context_lens.to(torch.int32).contiguous()
+        bt = block_tables.to(torch.int32).contiguous()
+        return self.fingerprint == _plan_fingerprint(lens, bt)
 
 
 def paged_max_rows(head_dim: int) -> int:
@@ -216,10 +259,11 @@ def paged_plan(context_lens: torch.Tensor, block_tables: torch.Tensor, *, Hq: in
     if n == 0:
         raise ValueError("paged_plan: unsupported shape")
     host = torch.empty(n, dtype=torch.int32)
-    split, key = paged_plan_fill(host, context_lens.cpu(), block_tables.cpu(), Hq=Hq, Hk=Hk, Lq=Lq, D=D,
-                                 num_blocks=num_blocks, block_size=block_size, max_context=max_context,
-                                 for_append=for_append)
-    return PagedPlan(host.to(device), split, key)
+    lens = context_lens.cpu().to(torch.int32).contiguous()
+    bt = block_tables.cpu().to(torch.int32).contiguous()
+    split, key = paged_plan_fill(host, lens, bt, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=num_blocks,
+                                 block_size=block_size, max_context=max_context, for_append=for_append)
+    return PagedPlan(host.to(device), split, key, _plan_fingerprint(lens, bt))
 
 
 def paged_workspace_bytes(B: int, Hq: int, Hk: int, Lq: int, D: int, block_size: int,
@@ -302,7 +346,12 @@ def paged_attention(
     lengths, block tables and shape (:func:`paged_plan`, or
     ``PagedKVCache.prepare_step``); the launch then reads every workgroup's
     share of the work from it instead of deriving it on the device
-    (``cie_paged_fwd_ex``), with the same result bit for bit.
+    (``cie_paged_fwd_ex``), with the same result bit for bit. With a plan,
+    ``block_tables`` and ``context_lens`` are checked for shape only and not
+    read: the plan carries the lengths and validated block ids it was built
+    from, so a plan of another step with the same shape attends over that
+    step's sequences (:meth:`PagedPlan.built_from` checks host copies). The
+    shape is checked here (its key) and by the launch (the plan's header).
     """
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_tables", block_tables), ("context_lens", context_lens)):

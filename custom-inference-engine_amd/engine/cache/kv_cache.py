@@ -350,9 +350,10 @@ class PagedKVCache:
         dev = host.to(self.device)
         plan = None
         if n_plan:
-            from engine.attention import PagedPlan
+            from engine.attention import PagedPlan, _plan_fingerprint
 
-            plan = PagedPlan(dev[p0:p0 + n_plan], split, key)
+            plan = PagedPlan(dev[p0:p0 + n_plan], split, key,
+                             _plan_fingerprint(host[o:o + B], host[:o].view(B, width)))
         return StepBatch(block_tables=dev[:o].view(B, width), context_lens=dev[o:o + B],
                          cu_new=dev[o + B:o + 2 * B + 1], starts=dev[o + 2 * B + 1:meta], num_new=num_new,
                          max_context=max_context, tables=tuple(tables), starts_host=tuple(starts),

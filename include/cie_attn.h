@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define CIE_ABI_VERSION 2
+#define CIE_ABI_VERSION 3
 
 enum cie_dtype { CIE_DTYPE_F16 = 0, CIE_DTYPE_BF16 = 1 };
 
@@ -68,6 +68,30 @@ int cie_abi_version(void);
 const char* cie_last_error(void);
 
 /*
+ * Compute units of the current device, as the library sizes its launches
+ * for it (queried once per device; 256, an unpartitioned MI355X, when no
+ * device can be queried). No reference counterpart.
+ */
+int cie_device_cus(void);
+
+/* Prefill kernels cie_flash_fwd chooses between (cie_prefill_kernel). */
+enum cie_prefill_kernel_kind {
+  CIE_PREFILL_32ROW = 0,       /* 32 query rows per wave, any head_dim but 128       */
+  CIE_PREFILL_HEAD_PAIRS = 1,  /* head_dim 64: the same 32 rows of two query heads   */
+  CIE_PREFILL_64ROW = 2,       /* head_dim 64: 64 rows of one query head per wave    */
+  CIE_PREFILL_INTERLEAVED = 3  /* head_dim 128: MFMA and softmax issued interleaved  */
+};
+
+/*
+ * The prefill kernel cie_flash_fwd runs for this launch shape (a
+ * CIE_PREFILL_* value), or a negative CIE_E* code for arguments
+ * cie_flash_fwd would reject. cu_count: compute units to size for, or <= 0
+ * for the current device's (cie_device_cus). No reference counterpart: a
+ * query for tests and profiles that must name the kernel they exercise.
+ */
+int cie_prefill_kernel(int B, int Hq, int Hk, int Lq, int Lk, int D, int causal, int dtype, int cu_count);
+
+/*
  * Dense attention: o = softmax(q k^T * scale [+ causal mask]) v.
  *   q: (B, Hq, Lq, D)   k, v: (B, Hk, Lk, D)   o: (B, Hq, Lq, D)
  * Reference: engine/attention.py:6-32 (argument checks :17-25, call :27-32)
@@ -81,10 +105,11 @@ int cie_flash_fwd(const void* q, const void* k, const void* v, void* o,
                   float scale, int causal, int dtype, void* stream);
 
 /*
- * Bytes of device workspace cie_paged_fwd needs for this shape (0 for an
- * unsupported shape): per-sequence piece descriptors and the partial states
- * of sequences split across workgroups. Any contents; calls that run
- * concurrently must not share a workspace.
+ * Bytes of device workspace cie_paged_fwd needs for this shape on the
+ * current device (0 for an unsupported shape): per-sequence piece
+ * descriptors and the partial states of sequences split across workgroups
+ * (the split follows the device's compute units). Any contents; calls that
+ * run concurrently must not share a workspace.
  * max_context bounds every context_lens[b]; pass <= 0 to use the table bound
  * max_blocks_per_seq * block_size (the value cie_paged_fwd uses the same way).
  * No reference counterpart: the reference never splits a context.
@@ -158,11 +183,16 @@ int cie_paged_plan(void* plan, size_t plan_bytes, const int32_t* context_lens, c
  * optional, the fused append (k_new, v_new non-NULL: cie_paged_fwd_append),
  * RoPE (rope_cos, rope_sin non-NULL: the _rope entries) and a device copy of
  * a plan from cie_paged_plan (plan non-NULL; plan_split = its return value;
- * block_tables and context_lens are then not read and may be NULL). The
- * results equal the corresponding entry's bit for bit. The workspace must
- * hold cie_paged_workspace_bytes bytes; with a plan whose plan_split is 0 it
- * may be NULL. A plan built for other arguments than this call's (checked
- * through its header on the device) gives NaN outputs.
+ * block_tables and context_lens are then not read and may be NULL: the plan
+ * holds the lengths and validated block ids it was built from, and a plan
+ * built from older lengths or tables attends over those). The results equal
+ * the corresponding entry's bit for bit. The workspace must hold
+ * cie_paged_workspace_bytes bytes; with a plan whose plan_split is 0 it may
+ * be NULL. The plan's header records B, Hq, Lq, head_dim, the head grouping,
+ * num_blocks, block_size, max_blocks_per_seq, the context bound, the fused
+ * append flag, the device's workgroup count and its split count; a plan
+ * whose header differs from this call's arguments (or from plan_split) is
+ * read no further and every output row is NaN.
  */
 int cie_paged_fwd_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
                      const int32_t* block_tables, const int32_t* context_lens, const void* plan, int plan_split,

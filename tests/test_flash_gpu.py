@@ -15,7 +15,8 @@ import torch
 from benchmarks import workloads
 from engine.attention import flash_attention
 from oracle import attention_rows_ref, flash_attention_ref, flash_attention_ref_chunked
-from prefill_dispatch import batch_for_two_row_groups, replicate, two_row_group_kernel_runs
+from engine.attention import prefill_kernel
+from prefill_dispatch import batch_for_two_row_groups, replicate
 
 pytestmark = pytest.mark.gpu
 
@@ -155,7 +156,7 @@ def test_gqa_equals_expanded_mha_bitwise(D, B, Lq, Lk):
     MHA (group size 1) runs 64-row waves of one head; the launcher decides
     from B * Hq alone, and both give every row the same bits."""
     if D == 64 and B >= 32:
-        assert two_row_group_kernel_runs(B, 8, Lq, Lk, True)
+        assert prefill_kernel(B, 8, 2, Lq, Lk, D, True) == "r64_heads"
     q, k, v = _inputs(B, 8, 2, Lq, Lk, D, torch.float16, seed=9)
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
     gqa = flash_attention(q, k, v, causal=True)

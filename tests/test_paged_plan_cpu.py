@@ -15,9 +15,16 @@ import pytest
 import torch
 
 from engine import _lib
-from engine.attention import paged_plan_fill, paged_plan_ints
+from engine.attention import device_cus, paged_plan_fill, paged_plan_ints
 
 TILE = 32
+
+
+def _xcds():
+    """XCDs of the device the plan is sized for: 32 active CUs per gfx950
+    XCD, at most 8, a power of two."""
+    n = min(max(device_cus() // 32, 1), 8)
+    return 1 << (n.bit_length() - 1)
 
 
 def _geometry(Hq, Hk, Lq, D):
@@ -83,9 +90,13 @@ def _check(lens, bt, Hq, Hk, Lq, D, num_blocks, bs, max_context=None, append=Fal
     Wg = int(P[3])
     NG = _geometry(Hq, Hk, Lq, D)
     W, NT, ranges, info, empty, split_ref = _restated(lens, bt.tolist(), num_blocks, bs, ctx_limit, Lq, append, Wg)
-    assert int(P[0]) == 0x43504C31 and int(P[1]) == W and int(P[2]) == NT and int(P[6]) == B
+    assert int(P[0]) == 0x43504C32 and int(P[1]) == W and int(P[2]) == NT and int(P[6]) == B
     assert int(P[7]) == (1 if append else 0)
     assert split == split_ref == int(P[5])
+    # the rest of the header: every argument the layout and the validated ids
+    # depend on, compared by the launch (NG, Lq, D, num_blocks, block_size,
+    # max_blocks, the context bound, Hq)
+    assert P[8:16].tolist() == [NG, Lq, D, num_blocks, bs, mb, ctx_limit, Hq]
     off_r = 16
     off_e = off_r + 8 * Wg
     off_i = off_e + 8 * (Wg + B)
@@ -117,30 +128,33 @@ def _check(lens, bt, Hq, Hk, Lq, D, num_blocks, bs, max_context=None, append=Fal
             assert tuple(f) == info[b], (gh, b, f, info[b])
     n_empty = int(P[4])
     assert [tuple(P[off_z + 2 * z: off_z + 2 * z + 2].tolist()) for z in range(n_empty)] == empty
-    # merge table: 8 lists of cap_t entries; every split sequence of every head
-    # group exactly once, each list at most merge_cap(split * NG) long, each
-    # sequence on the XCD that ran its middle piece unless that list was full
+    # merge table: 8 lists of cap_t entries (those of XCDs the device does not
+    # have stay empty); every split sequence of every head group exactly
+    # once, each list at most merge_cap(split * NG) long, each sequence on the
+    # XCD that ran its middle piece unless that list was full
+    nx = _xcds()
     off_m = off_z + 2 * B
-    cap_t = (B * NG + 7) // 8 + 1
-    cap = (split * NG + 7) // 8 + 1
+    cap_t = (B * NG + nx - 1) // nx + 1
+    cap = (split * NG + nx - 1) // nx + 1
     assert P.numel() == off_m + 8 * cap_t
     n_wg = NG * Wg
-    base, extra = n_wg // 8, n_wg % 8
+    base, extra = n_wg // nx, n_wg % nx
 
     def xcd_of(logical):  # the main pass's XCD of range j of head group gh (logical = gh Wg + j)
-        return next(x for x in range(8) if logical < (x + 1) * base + min(x + 1, extra)) if logical < n_wg else 7
+        return next(x for x in range(nx) if logical < (x + 1) * base + min(x + 1, extra)) if logical < n_wg else nx - 1
 
     placed, fallbacks = {}, 0
     for x in range(8):
         lst = P[off_m + x * cap_t: off_m + (x + 1) * cap_t].tolist()
         used = [u for u in lst if u >= 0]
         assert lst == used + [-1] * (cap_t - len(used)) and len(used) <= cap, (x, lst)
+        assert x < nx or not used
         for u in used:
             assert u not in placed, u
             placed[u] = x
     # (only launches of one workgroup per CU or fewer place ranges in XCD runs
     # and fill the table; the others merge in grid order)
-    runs = NG * Wg <= 256
+    runs = NG * Wg <= device_cus()
     want = {b * NG + gh for b in range(B) for gh in range(NG) if info[b][1] > 1} if runs else set()
     assert set(placed) == want
     for u, x in placed.items():

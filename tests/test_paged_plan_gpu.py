@@ -96,28 +96,69 @@ def test_planned_fused_append_equals_unplanned(Lq, dtype, rope):
     assert torch.equal(pools[0][0], pools[1][0]) and torch.equal(pools[0][1], pools[1][1])
 
 
-def test_plan_for_other_arguments_is_rejected_or_gives_nan():
-    q, kp, vp, bt, lt = make_paged([40, 300], 1, 64, torch.float16, 16, seed=5)
-    args = [t.to(DEV) for t in (q, kp, vp, bt, lt)]
-    pl = paged_plan(lt, bt, Hq=8, Hk=2, Lq=1, D=64, num_blocks=kp.shape[0], block_size=16, for_append=True,
-                    device=DEV)
-    with pytest.raises(ValueError):  # the Python layer checks the key
-        paged_attention(*args, plan=pl)
-    # through the C ABI the device checks the plan's header: a plan built for the fused
-    # append used by a plain launch gives NaN rows rather than reading past anything
-    lib = _lib.load()
-    o = torch.zeros_like(args[0])
+def _launch_ex(lib, args, o, plan, split, *, Hq, Hk, Lq, D, nb, bs, mb, max_context):
+    """cie_paged_fwd_ex straight through the C ABI (no Python key check)."""
     st = [_lib.strides(t) for t in (args[0], args[1], args[2], o)]
     none3 = (ctypes.c_int64 * 3)(0, 0, 1)
-    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    ws = torch.empty(16 << 20, dtype=torch.uint8, device=DEV)
     rc = lib.cie_paged_fwd_ex(args[0].data_ptr(), None, None, args[1].data_ptr(), args[2].data_ptr(), None, None,
-                              pl.data.data_ptr(), pl.split, o.data_ptr(), ws.data_ptr(), ws.numel(),
-                              st[0], none3, none3, st[1], st[2], st[3], 2, 8, 2, 1, 64, kp.shape[0], 16, bt.shape[1],
-                              0, ctypes.c_float(0.125), 1, 0, None, None, 0, 0,
+                              plan.data_ptr(), split, o.data_ptr(), ws.data_ptr(), ws.numel(),
+                              st[0], none3, none3, st[1], st[2], st[3], args[0].shape[0], Hq, Hk, Lq, D, nb, bs,
+                              mb, max_context, ctypes.c_float(1.0 / math.sqrt(D)), 1, 0, None, None, 0, 0,
                               _lib.stream_handle(torch.device(DEV)))
     _lib.check(rc)
     torch.cuda.synchronize()
-    assert torch.isnan(o).all()
+
+
+# one argument of the plan builder changed per case: (field, builder overrides, plan_split offset)
+_MISMATCHES = [
+    ("append", dict(for_append=True), 0),
+    ("B", dict(rows=1), 0),
+    ("Hq", dict(Hq=4), 0),
+    ("Lq", dict(Lq=2), 0),
+    ("head_dim", dict(D=32), 0),
+    ("num_blocks", dict(num_blocks_add=7), 0),
+    ("block_size", dict(block_size=8), 0),
+    ("max_blocks", dict(extra_col=True), 0),
+    ("max_context", dict(max_context=301), 0),
+    ("head groups", dict(Hq=8, Hk=8), 0),
+    ("split count", dict(), 1),
+]
+
+
+@pytest.mark.parametrize("field,over,dsplit", _MISMATCHES, ids=[m[0] for m in _MISMATCHES])
+def test_plan_for_other_arguments_gives_nan(field, over, dsplit):
+    """Through the C ABI a plan is checked against the launch on the device
+    (its header): a plan built with any one argument different from the
+    launch's, or passed with another split count, is read no further and
+    every output row is NaN (the Python layer refuses such a plan by its key
+    before that)."""
+    Hq, Hk, Lq, D, bs = 8, 2, 1, 64, 16
+    q, kp, vp, bt, lt = make_paged([40, 300], Lq, D, torch.float16, bs, Hq=Hq, Hk=Hk, seed=5)
+    nb, mb = kp.shape[0], bt.shape[1]
+    args = [t.to(DEV) for t in (q, kp, vp, bt, lt)]
+    lib = _lib.load()
+    # the matching plan: the same result as the unplanned launch
+    good = paged_plan(lt, bt, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb, block_size=bs, device=DEV)
+    assert good.split > 0  # the 300-token sequence is split, so the merge pass runs
+    o = torch.zeros_like(args[0])
+    _launch_ex(lib, args, o, good.data, good.split, Hq=Hq, Hk=Hk, Lq=Lq, D=D, nb=nb, bs=bs, mb=mb, max_context=0)
+    assert torch.equal(o, paged_attention(*args, causal=True))
+    with pytest.raises(ValueError):  # the Python layer checks the key
+        paged_attention(*args, plan=paged_plan(lt, bt, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb, block_size=bs,
+                                               for_append=True, device=DEV))
+    rows = over.get("rows", 2)
+    btp = bt[:rows]
+    if over.get("extra_col"):
+        btp = torch.cat([btp, torch.zeros(rows, 1, dtype=torch.int32)], dim=1)
+    bad = paged_plan(lt[:rows], btp, Hq=over.get("Hq", Hq), Hk=over.get("Hk", Hk), Lq=over.get("Lq", Lq),
+                     D=over.get("D", D), num_blocks=nb + over.get("num_blocks_add", 0),
+                     block_size=over.get("block_size", bs), max_context=over.get("max_context"),
+                     for_append=over.get("for_append", False), device=DEV)
+    o = torch.zeros_like(args[0])
+    _launch_ex(lib, args, o, bad.data, bad.split + dsplit, Hq=Hq, Hk=Hk, Lq=Lq, D=D, nb=nb, bs=bs, mb=mb,
+               max_context=0)
+    assert torch.isnan(o).all(), field
 
 
 def test_attention_section_with_step_plan_equals_without():

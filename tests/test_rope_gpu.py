@@ -18,7 +18,8 @@ import math
 import pytest
 import torch
 
-from prefill_dispatch import batch_for_two_row_groups, two_row_group_kernel_runs
+from engine.attention import prefill_kernel
+from prefill_dispatch import batch_for_two_row_groups
 from engine.attention import flash_attention, paged_attention
 from engine.cache import KVCacheConfig, PagedKVCache, kv_append
 from engine.model.rope import RotaryEmbedding, build_rope_cache, rope_apply
@@ -194,7 +195,7 @@ def test_flash_with_fused_q_rope_two_row_groups(dtype, tables):
     ref = flash_attention_ref(qr.float(), kr.float(), v.float(), causal=True)
     R = (batch_for_two_row_groups(Hq, L, L, True) + B0 - 1) // B0  # copies of the 2-problem batch
     B = B0 * R
-    assert two_row_group_kernel_runs(B, Hq, L, L, True)
+    assert prefill_kernel(B, Hq, Hk, L, L, D, True, dtype) == "r64_heads"
     rep = lambda t: t.repeat(R, *([1] * (t.dim() - 1)))  # noqa: E731
     qd, krd, vd, pd = rep(q).to(DEV), rep(kr).to(DEV), rep(v).to(DEV), rep(pos0).to(DEV)
     fused = flash_attention(qd, krd, vd, causal=True, rope=(cd, sd), q_pos0=pd)
@@ -222,7 +223,7 @@ def test_flash_fused_q_rope_positions_past_the_table(dtype):
     v = torch.randn(B0, Hk, L, D, generator=g).to(dtype)
     pos0 = torch.tensor([0, rows - 150], dtype=torch.int32)  # batch 1: rows 150.. lie past the table
     R = (batch_for_two_row_groups(Hq, L, L, True) + B0 - 1) // B0
-    assert two_row_group_kernel_runs(B0 * R, Hq, L, L, True)
+    assert prefill_kernel(B0 * R, Hq, Hk, L, L, D, True, dtype) == "r64_heads"
     rep = lambda t: t.repeat(R, *([1] * (t.dim() - 1)))  # noqa: E731
     qd, kd, vd, pd = rep(q).to(DEV), rep(k).to(DEV), rep(v).to(DEV), rep(pos0).to(DEV)
     fused = flash_attention(qd, kd, vd, causal=True, rope=(cd, sd), q_pos0=pd)

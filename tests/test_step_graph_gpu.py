@@ -11,7 +11,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-from prefill_dispatch import batch_for_two_row_groups, two_row_group_kernel_runs
+from engine.attention import prefill_kernel
+from prefill_dispatch import batch_for_two_row_groups
 from engine.cache import KVCacheConfig, PagedKVCache
 from engine.model import attention_section
 
@@ -78,7 +79,7 @@ def test_out_argument_writes_views_in_place():
     # 200 rows over a batch that takes the head_dim-64 two-row-group kernel
     Lr = 200
     Br = batch_for_two_row_groups(Hq, Lr, Lr, True)
-    assert two_row_group_kernel_runs(Br, Hq, Lr, Lr, True)
+    assert prefill_kernel(Br, Hq, Hk, Lr, Lr, D, True) == "r64_heads"
     qr, kr, vr = (torch.randn(Br, h, Lr, D, generator=g).half().to(DEV) for h in (Hq, Hk, Hk))
     big = torch.full((Br, Lr, Hq, D), 7.0, dtype=torch.float16, device=DEV)
     flash_attention(qr, kr, vr, causal=True, out=big.transpose(1, 2))
