@@ -25,9 +25,10 @@
 // x operand takes x[m_r][16h .. 16h+16) split the same way, so MFMA 0
 // contracts k in {0..7, 16..23} and MFMA 1 k in {8..15, 24..31}.
 //
-// Kernels by M: 1 a VALU dot-product kernel, up to 64 a weight-streaming
-// MFMA kernel (both one launch, no workspace; below), above that the tiled
-// kernel described here.
+// Kernels by M: up to 2 a row-streaming VALU dot kernel with the activations
+// in LDS (a VALU dot kernel reading them from L2 when they do not fit), up to
+// 64 a weight-streaming MFMA kernel (all one launch, no workspace; below),
+// above that the tiled kernel described here.
 //
 // Any K. The reference masks the K tail of its last tile
 // (kernels/int8_matmul.py:43-50). Here each kernel's main loop covers the
@@ -619,9 +620,11 @@ static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Decode at M = 1: VALU dot products. The MFMA operand of the kernel above
-// spans 32 activation rows, so at M = 1 it computes 32x the products it
-// keeps and still loads each wave's whole K share before its first MFMA.
+// Decode at M = 1 when the activation row does not fit the LDS of the
+// row-streaming kernel below (K > 32768): VALU dot products. The MFMA
+// operand of the kernel above spans 32 activation rows, so at M = 1 it
+// computes 32x the products it keeps and still loads each wave's whole K
+// share before its first MFMA.
 // Here a single-wave workgroup streams kDotRows weight rows in 1 KiB chunks
 // (lane l covers k = 1024 c + 16 l .. +16 of chunk c: one 16-byte load per
 // row and chunk, the contiguous-run pattern), kDotDepth chunks ahead in a
@@ -632,7 +635,9 @@ static hipError_t launch_ws_t(const I8GemmParams& p, hipStream_t stream) {
 // and lane r * MC + m finishes output (m, n0 + r). Two rows per wave and two
 // chunks ahead measured fastest at M = 1-4 among 1-16 rows and 2-8 chunks
 // (more waves in flight beat deeper per-wave rings); from M = 2 the MFMA
-// streaming kernel above is faster.
+// streaming kernel above is faster. The row-streaming kernel below, which
+// stages the activations in LDS instead, runs N = K = 4096 in 5.06 us
+// against 5.36.
 constexpr int kDotRows = 2;
 constexpr int kDotDepth = 2;
 constexpr int kDotMaxM = 1;  // from M = 2 the MFMA streaming kernel is faster
@@ -725,6 +730,131 @@ __global__ __launch_bounds__(64) void int8_gemv_dot_kernel(const I8GemmParams p)
   }
 }
 
+// Decode at M <= kRvMaxM: every weight byte loaded once, all of a wave's
+// loads in flight together, the activations read from LDS. A workgroup of
+// NWV waves owns RPW = 64 / SL weight rows; its waves split the K steps
+// (KSTEP = 16 SL columns each) into NWV contiguous shares, and within a wave
+// lane (r = lane / SL, j = lane % SL) takes 16 contiguous bytes of row r per
+// step (k = KSTEP s + 16 j: the SL lanes of a row read one contiguous
+// KSTEP-byte run). The activation rows (MC of them, the K prefix the steps
+// cover) are copied into LDS once per workgroup by direct-to-LDS loads
+// issued before the weight loads, so the only loads per step are the
+// weights (the VALU dot kernel above reloads the activation fragments from
+// L2 next to every weight chunk). Each wave keeps kRvDepth steps of weight
+// loads in flight in a register ring; products are exact in fp32 (v_dot2 on
+// the dequantized pairs), a lane's terms are summed in ascending k, the SL
+// lanes of a row by a fixed xor butterfly and the waves of the workgroup in
+// wave order through LDS (deterministic); the K tail past the steps is added
+// last, in ascending k. N = K = 4096, graph replay (us; the dot kernel 5.36
+// at M = 1, the MFMA streaming kernel 5.74 at M = 2, 5.77 at M = 4):
+// SL x NWV x depth 4x8x8 6.55, 8x8x8 5.29, 8x8x4 5.22, 8x8x2 5.14, 16x8x8 5.36,
+// 16x4x8 5.52, 32x4x8 5.43, 8x16x2 5.06-5.10 (M = 2: 5.64), 8x16x4 5.18,
+// 16x16x2 6.76; at M = 3-4 (four staged rows) 6.77, slower than the MFMA
+// streaming kernel, so it takes M <= 2.
+constexpr int kRvWaves = 16;
+constexpr int kRvSL = 8;
+constexpr int kRvDepth = 2;
+constexpr int kRvMaxM = 2;
+constexpr int kRvMaxLds = 64 * 1024;  // activation bytes staged per workgroup
+constexpr int rv_rows(int M) { return M <= 1 ? 1 : 2; }  // activation rows a launch stages
+
+template <int MC, int SL>
+struct RvCfg {
+  static constexpr int RPW = 64 / SL;     // weight rows per workgroup
+  static constexpr int KSTEP = 16 * SL;   // k per step
+  static int kmain(int K) { return K - K % KSTEP; }
+  static int kpad(int K) { return (kmain(K) + 511) / 512 * 512; }  // LDS row pitch (elements, 1 KiB units)
+  static size_t lds(int K) { return (size_t)MC * kpad(K) * 2; }
+};
+
+template <int DTYPE, int MC, int SL, int NWV>
+__global__ __launch_bounds__(64 * NWV) void int8_gemv_rows_kernel(const I8GemmParams p) {
+  using E = Elt<DTYPE>;
+  using C = RvCfg<MC, SL>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t rv_lds[];
+  __shared__ float part[NWV][MC][C::RPW];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane / SL, j = lane % SL;
+  const int n0 = blockIdx.x * C::RPW;
+  const int KM = p.K - p.K % C::KSTEP, KP = (KM + 511) / 512 * 512;
+  const int S = KM / C::KSTEP;
+  const int s0 = w * S / NWV, ns = (w + 1) * S / NWV - s0;  // this wave's steps (uniform)
+
+  // activation rows -> LDS: 1 KiB units (64 chunks of 16 bytes) of row m,
+  // unit u at byte 2 (m KP + 512 u); lanes past the row's KM / 8 chunks
+  // copy its last chunk into the row's padding
+  const uint32_t xl = lds_addr_of(rv_lds);
+  const int upr = KP / 512, nu = MC * upr;
+  for (int v = w; v < nu; v += NWV) {
+    const int m = v / upr, u = v - m * upr;
+    const int c = min(64 * u + lane, KM / 8 - 1);
+    dma16_at(p.x + (int64_t)min(m, p.M - 1) * p.xs + 8 * c, xl + 2u * (uint32_t)(m * KP + 512 * u));
+  }
+  // weight loads of the first kRvDepth steps (rows past N clamped: loaded, never stored)
+  const int8_t* wrow = p.w + (int64_t)min(n0 + r, p.N - 1) * p.wsr + 16 * j;
+  u32x4 wq[kRvDepth];
+  gv_static_for<kRvDepth>([&](auto I) CIE_GV_INLINE {
+    constexpr int i = decltype(I)::value;
+    if (i < ns) wq[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + C::KSTEP * (s0 + i)));
+  });
+  // this wave's activation copies landed (the weight loads were issued after them)
+  wait_steps_ahead<1, kRvDepth>(min(ns, kRvDepth));
+  __syncthreads();  // every wave's copies landed
+
+  float acc[MC];
+#pragma unroll
+  for (int m = 0; m < MC; ++m) acc[m] = 0.f;
+  for (int q0 = 0; q0 < ns; q0 += kRvDepth) {
+    gv_static_for<kRvDepth>([&](auto I) CIE_GV_INLINE {
+      constexpr int i = decltype(I)::value;
+      const int q = q0 + i;
+      if (q < ns) {  // wave-uniform
+        u32x4 a0, a1;
+        dequant16<DTYPE>(wq[i], a0, a1);
+        if (q + kRvDepth < ns)
+          wq[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + C::KSTEP * (s0 + q + kRvDepth)));
+        const int k = C::KSTEP * (s0 + q) + 16 * j;
+#pragma unroll
+        for (int m = 0; m < MC; ++m) {
+          const uint8_t* xb = rv_lds + 2 * (m * KP + k);
+          const u32x4 x0 = *reinterpret_cast<const u32x4*>(xb);
+          const u32x4 x1 = *reinterpret_cast<const u32x4*>(xb + 16);
+          float t = acc[m];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t = E::dot2(a0[e], x0[e], t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t = E::dot2(a1[e], x1[e], t);
+          acc[m] = t;
+        }
+      }
+    });
+  }
+#pragma unroll
+  for (int m = 0; m < MC; ++m) {
+    float v = acc[m];
+#pragma unroll
+    for (int off = 1; off < SL; off <<= 1) v += __shfl_xor(v, off);
+    if (j == 0) part[w][m][r] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < MC * C::RPW) {
+    const int m = threadIdx.x / C::RPW, rr = threadIdx.x % C::RPW, n = n0 + rr;
+    float out = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < NWV; ++wv) out += part[wv][m][rr];
+    if (m < p.M && n < p.N) {
+      if (KM < p.K) out += tail_dot<DTYPE>(p, m, n, KM);
+      float t = out * load_scale(p.scales, n, p.scale_dtype);
+      if (p.bias) {  // the reference adds the bias to the rounded product, in the output dtype
+        const uint32_t rb = Elt<DTYPE>::pack2(t, 0.f);
+        t = elt_to_f32<DTYPE>((uint16_t)rb) + elt_to_f32<DTYPE>(p.bias[n]);
+      }
+      p.y[(int64_t)m * p.ys + n] = (uint16_t)Elt<DTYPE>::pack2(t, 0.f);
+    }
+  }
+}
+
 I8Geom int8_gemm_geometry(int M, int N, int K, DeviceShape dev) {
   I8Geom g{};
   g.dev = dev;
@@ -732,6 +862,7 @@ I8Geom int8_gemm_geometry(int M, int N, int K, DeviceShape dev) {
   g.ksteps = K / kI8BK;
   if (M <= 64) {  // weight streaming, one launch, no workspace (2: VALU dot products)
     g.gemv = M <= kDotMaxM ? 2 : 1;
+    if (M <= kRvMaxM && (size_t)rv_rows(M) * RvCfg<1, kRvSL>::lds(K) <= (size_t)kRvMaxLds) g.gemv = 3;
     g.mt = M <= 32 ? 1 : 2;
     g.m_tiles = 1;
     g.splits = 1;
@@ -788,8 +919,22 @@ static hipError_t launch_i8_t(const I8GemmParams& p, size_t lds, bool kw2, hipSt
   return hipGetLastError();
 }
 
+template <int DTYPE, int MC>
+static hipError_t launch_rv_t(const I8GemmParams& p, hipStream_t stream) {
+  using C = RvCfg<MC, kRvSL>;
+  const size_t lds = C::lds(p.K);
+  if (lds > (size_t)kRvMaxLds) return hipErrorInvalidValue;  // geometry and kernel disagree
+  const void* fn = reinterpret_cast<const void*>(&int8_gemv_rows_kernel<DTYPE, MC, kRvSL, kRvWaves>);
+  const hipError_t attr = set_dynamic_lds(fn, kRvMaxLds);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((int8_gemv_rows_kernel<DTYPE, MC, kRvSL, kRvWaves>), dim3((unsigned)((p.N + C::RPW - 1) / C::RPW)),
+                     dim3(64 * kRvWaves), lds, stream, p);
+  return hipGetLastError();
+}
+
 template <int DTYPE>
 static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_t stream) {
+  if (g.gemv == 3) return p.M == 1 ? launch_rv_t<DTYPE, 1>(p, stream) : launch_rv_t<DTYPE, 2>(p, stream);
   if (g.gemv == 2) {
     const dim3 grid((unsigned)((p.N + kDotRows - 1) / kDotRows));
     hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 1>), grid, dim3(64), 0, stream, p);

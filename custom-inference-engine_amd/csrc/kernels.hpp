@@ -267,7 +267,8 @@ struct I8GemmParams {
 // Launch geometry of an INT8 GEMM; a pure function of (M, N, K), so the
 // workspace query and the launch agree.
 struct I8Geom {
-  int gemv;                // 1: weight-streaming MFMA kernel (M <= 64), 2: VALU dot kernel (M = 1); one launch
+  int gemv;                // 1: weight-streaming MFMA kernel (M <= 64), 2: VALU dot kernel (M = 1),
+                           // 3: row-streaming dot kernel (M <= 2, activations staged in LDS); one launch
   int kw2;                 // tiled kernel: two K-waves per workgroup (eight waves)
   DeviceShape dev;         // the GPU the launch is sized for
   int mt;                  // 32-row activation tiles per workgroup

@@ -52,8 +52,11 @@ def _exact_case(M, N, K, dtype, seed, bias):
 @pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (512, 4096, 4096), (1, 4096, 4096), (33, 300, 640),
                                    (100, 127, 64), (2048, 4096, 256), (515, 1000, 1024), (16, 11008, 4096),
                                    (32, 4096, 11008), (5, 96, 64), (31, 1000, 2112),
-                                   # the dot-product kernel (M <= 4): ragged N, K tails within a 1 KiB chunk
+                                   # small M: ragged N, K tails within a step
                                    (2, 300, 640), (3, 1001, 2112), (4, 130, 1088), (1, 7, 64), (1, 11008, 4096),
+                                   # M = 1, 2 with the whole activation rows in LDS (K = 32768, 16384), and
+                                   # past it (the kernels that read the activations from L2)
+                                   (1, 64, 32768), (1, 80, 32800), (2, 64, 16384), (2, 48, 16448),
                                    # the streaming kernel at 8 / 16 / 32 / 64 staged rows, K tails within a pass
                                    (8, 4096, 4096), (12, 520, 1216), (40, 333, 1088), (64, 1000, 4160), (65, 512, 1024),
                                    # any K (the reference masks the K tail, kernels/int8_matmul.py:43-50):
