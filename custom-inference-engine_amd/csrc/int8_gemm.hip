@@ -428,7 +428,8 @@ __global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParam
   store4<DTYPE>(p, m, n, finish4<DTYPE>(a, p, n));
 }
 
-// Decode-sized layers (1 < M <= 64): weight streaming in one launch. A
+// Decode-sized layers (2 < M <= 64, and M <= 2 with activation rows too long
+// for the row-streaming kernel's LDS): weight streaming in one launch. A
 // workgroup owns kGvRows = 16 weight rows and its 4 waves split K into
 // quarters. A wave streams its quarter in passes of PG 32-k groups: per pass
 // WI direct-to-LDS loads move the 16 weight rows (32 PG contiguous bytes of
@@ -441,7 +442,10 @@ __global__ __launch_bounds__(256) void int8_gemm_reduce_kernel(const I8GemmParam
 // Chunks are XOR-swizzled by row so the fragment reads spread over the LDS
 // banks. The products run on 16x16x32 MFMAs (see the kernel); the 4 waves'
 // partial tiles are summed through LDS in wave order (deterministic), then
-// scaled, rounded, stored.
+// scaled, rounded, stored. Staging 4 rows instead of 8 at M = 3-4 halves the
+// activation copies (N = K = 4096: 5.61 / 5.65 us against 5.75 / 5.79);
+// eight or sixteen waves per workgroup (K in eighths or sixteenths, two
+// to four pass buffers per wave) ran 1-9 % slower at M = 3-16.
 constexpr int kGvWaves = 4;
 constexpr int kGvRows = 16;
 
@@ -940,7 +944,8 @@ static hipError_t launch_i8_d(const I8GemmParams& p, const I8Geom& g, hipStream_
     hipLaunchKernelGGL((int8_gemv_dot_kernel<DTYPE, 1>), grid, dim3(64), 0, stream, p);
     return hipGetLastError();
   }
-  if (g.gemv) {  // staged activation rows: 8, 16, 32 or 64
+  if (g.gemv) {  // staged activation rows: 4, 8, 16, 32 or 64
+    if (p.M <= 4) return launch_ws_t<DTYPE, 4, 1, 1>(p, stream);
     if (p.M <= 8) return launch_ws_t<DTYPE, 8, 1, 1>(p, stream);
     if (p.M <= 16) return launch_ws_t<DTYPE, 16, 1, 1>(p, stream);
     if (p.M <= 32) return launch_ws_t<DTYPE, 32, 1, 2>(p, stream);
