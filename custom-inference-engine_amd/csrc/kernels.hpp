@@ -141,7 +141,7 @@ struct PagedGeom {
 PagedGeom paged_geometry(int B, int Hq, int Hk, int Lq, int D, int ctx_limit, int block_size, DeviceShape dev);
 
 // Host-built plan of a paged launch (see paged_plan.cpp for the layout).
-constexpr int32_t kPlanMagic = 0x43504c32;  // "CPL2"
+constexpr int32_t kPlanMagic = 0x43504c33;  // "CPL3"
 constexpr int kPlanHeader = 16;             // header ints
 // Header fields (int32 indices): every argument the plan's layout, ranges
 // and validated block ids depend on, compared by the launch before it reads
@@ -161,8 +161,10 @@ struct PlanLayout {
 // keeps what its workgroups wrote in its L2 across the kernel boundary), and
 // the plan's merge table hands each split sequence's merge work to the XCD
 // holding its pieces: mtab[x][i] (x < kMaxXcds, i < merge_table_cap(...)) is
-// the i-th sequence (b * NG + gh) merged on XCD x, -1 when unused (lists of
-// XCDs the device does not have stay empty).
+// the i-th sequence merged on XCD x as 4 ints: b * NG + gh, then the
+// sequence's piece descriptor (first range, pieces, slot side of piece 0),
+// so a merge workgroup reads its whole schedule in one load; {-1, 0, 0, 0}
+// when unused (lists of XCDs the device does not have stay empty).
 constexpr int kMaxXcds = 8;
 // Sequences per XCD list over 2^xcd_shift XCDs: every split sequence fits,
 // with one to spare.

@@ -764,13 +764,18 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   // and the offsets of its descriptors and merge table may lie past its end
   if (p.plan && !plan_matches<D>(p)) return;
   int unit = -1;
+  int4 minf = {0, 0, 0, 0};  // the table entry's piece descriptor
   if (p.mtab_cap > 0) {
     const uint32_t per_unit = (uint32_t)p.NWV * p.Rt * Q4 * kMergeLanes;
     const uint32_t wpu = (per_unit + 255) / 256;
     const uint32_t slot = blockIdx.x >> p.xcd_shift, ui = slot / wpu;
     const int xcd = (int)(blockIdx.x & ((1u << p.xcd_shift) - 1));
-    if (ui < (uint32_t)p.mtab_cap)
-      unit = p.plan[p.plan_mtab + (int64_t)xcd * merge_table_cap(p.B, p.NG, p.xcd_shift) + ui];
+    if (ui < (uint32_t)p.mtab_cap) {
+      const int4 e = reinterpret_cast<const int4*>(p.plan + p.plan_mtab)
+          [(int64_t)xcd * merge_table_cap(p.B, p.NG, p.xcd_shift) + ui];
+      unit = e.x;
+      minf = int4{e.y, e.z, e.w, 0};
+    }
     if (unit < 0 || unit >= p.B * p.NG) return;  // an unused (or invalid) entry: the whole workgroup idles
     tid = (slot - ui * wpu) * 256u + threadIdx.x;
   }
@@ -798,7 +803,7 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   }
   // Items of one wave belong to at most a few sequences; lanes past the end
   // or without work still take part in the shuffles below.
-  const int4 inf = in ? p.info[(int64_t)gh * p.B + b] : int4{0, 0, 0, 0};
+  const int4 inf = unit >= 0 ? minf : (in ? p.info[(int64_t)gh * p.B + b] : int4{0, 0, 0, 0});
   const int pieces = inf.y;
   const int hh = w % p.Hg, qt = w / p.Hg;
   const int r = qt * 32 + row;

@@ -33,9 +33,11 @@
 //            merge pass's piece descriptors), zero for unsplit sequences
 //   empty    B rows of 2: sequences without tiles (b, 1 if the history is
 //            empty, 0 if its length is invalid)
-//   mtab     kMaxXcds lists of merge_table_cap(B, NG, xcd_shift): the split
-//            sequences (b * NG + gh) whose merge runs on each XCD, -1 past
-//            the end (and in the lists of XCDs the device does not have);
+//   mtab     (int4 aligned) kMaxXcds lists of merge_table_cap(B, NG,
+//            xcd_shift) entries of 4 ints: the split sequences (b * NG + gh,
+//            then its info descriptor) whose merge runs on each XCD,
+//            {-1, 0, 0, 0} past the end (and in the lists of XCDs the device
+//            does not have);
 //            each goes to the XCD that ran its middle piece (its partial
 //            states are in that XCD's L2), or, when that list holds
 //            merge_cap(split sequences) already, to the shortest list
@@ -55,8 +57,8 @@ PlanLayout paged_plan_layout(const PagedGeom& g, int B, int max_blocks) {
   L.info = L.ids + (size_t)B * max_blocks + (size_t)2 * g.Wg;
   L.info = (L.info + 3) / 4 * 4;  // int4 aligned
   L.empty = L.info + (size_t)4 * g.NG * B;
-  L.mtab = L.empty + (size_t)2 * B;
-  L.ints = L.mtab + (size_t)kMaxXcds * merge_table_cap(B, g.NG, g.dev.xcd_shift);
+  L.mtab = (L.empty + (size_t)2 * B + 3) / 4 * 4;  // int4 aligned
+  L.ints = L.mtab + (size_t)4 * kMaxXcds * merge_table_cap(B, g.NG, g.dev.xcd_shift);
   return L;
 }
 
@@ -152,7 +154,7 @@ int build_paged_plan(int32_t* P, const PagedGeom& g, const PlanLayout& L, const 
     const int xs = g.dev.xcd_shift, nx = 1 << xs;
     const int cap_t = merge_table_cap(B, g.NG, xs), cap = merge_cap(split * g.NG, xs);
     int32_t* T = P + L.mtab;
-    for (int i = 0; i < kMaxXcds * cap_t; ++i) T[i] = -1;
+    for (int i = 0; i < kMaxXcds * cap_t; ++i) T[4 * i] = -1;  // (the descriptor ints stay 0)
     if (paged_xcd_runs(g)) {
       int cnt[kMaxXcds] = {0, 0, 0, 0, 0, 0, 0, 0};
       const int64_t n = (int64_t)g.NG * g.Wg;
@@ -162,7 +164,11 @@ int build_paged_plan(int32_t* P, const PagedGeom& g, const PlanLayout& L, const 
           if (tiles[b] == 0 || f[1] <= 1) continue;
           int x = xcd_of_logical((int64_t)gh * g.Wg + f[0] + f[1] / 2, n, xs);
           if (cnt[x] >= cap) x = (int)(std::min_element(cnt, cnt + nx) - cnt);
-          T[x * cap_t + cnt[x]++] = b * g.NG + gh;
+          int32_t* t = T + (size_t)4 * (x * cap_t + cnt[x]++);
+          t[0] = b * g.NG + gh;
+          t[1] = f[0];
+          t[2] = f[1];
+          t[3] = f[2];
         }
     }
   }

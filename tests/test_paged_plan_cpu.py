@@ -90,7 +90,7 @@ def _check(lens, bt, Hq, Hk, Lq, D, num_blocks, bs, max_context=None, append=Fal
     Wg = int(P[3])
     NG = _geometry(Hq, Hk, Lq, D)
     W, NT, ranges, info, empty, split_ref = _restated(lens, bt.tolist(), num_blocks, bs, ctx_limit, Lq, append, Wg)
-    assert int(P[0]) == 0x43504C32 and int(P[1]) == W and int(P[2]) == NT and int(P[6]) == B
+    assert int(P[0]) == 0x43504C33 and int(P[1]) == W and int(P[2]) == NT and int(P[6]) == B
     assert int(P[7]) == (1 if append else 0)
     assert split == split_ref == int(P[5])
     # the rest of the header: every argument the layout and the validated ids
@@ -133,10 +133,10 @@ def _check(lens, bt, Hq, Hk, Lq, D, num_blocks, bs, max_context=None, append=Fal
     # once, each list at most merge_cap(split * NG) long, each sequence on the
     # XCD that ran its middle piece unless that list was full
     nx = _xcds()
-    off_m = off_z + 2 * B
+    off_m = (off_z + 2 * B + 3) // 4 * 4
     cap_t = (B * NG + nx - 1) // nx + 1
     cap = (split * NG + nx - 1) // nx + 1
-    assert P.numel() == off_m + 8 * cap_t
+    assert P.numel() == off_m + 4 * 8 * cap_t
     n_wg = NG * Wg
     base, extra = n_wg // nx, n_wg % nx
 
@@ -145,13 +145,17 @@ def _check(lens, bt, Hq, Hk, Lq, D, num_blocks, bs, max_context=None, append=Fal
 
     placed, fallbacks = {}, 0
     for x in range(8):
-        lst = P[off_m + x * cap_t: off_m + (x + 1) * cap_t].tolist()
+        ent = P[off_m + 4 * x * cap_t: off_m + 4 * (x + 1) * cap_t].reshape(cap_t, 4).tolist()
+        lst = [e[0] for e in ent]
         used = [u for u in lst if u >= 0]
         assert lst == used + [-1] * (cap_t - len(used)) and len(used) <= cap, (x, lst)
         assert x < nx or not used
-        for u in used:
+        for u, e in zip(used, ent):
             assert u not in placed, u
             placed[u] = x
+            # each entry carries its sequence's piece descriptor (the info rows)
+            assert tuple(e[1:]) == info[u // NG], (x, e, info[u // NG])
+        assert all(e == [-1, 0, 0, 0] for e in ent[len(used):]), (x, ent)
     # (only launches of one workgroup per CU or fewer place ranges in XCD runs
     # and fill the table; the others merge in grid order)
     runs = NG * Wg <= device_cus()
