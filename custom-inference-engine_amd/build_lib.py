@@ -21,6 +21,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libcie_attn.so")
+RATES_PATH = os.path.join(BUILD, "vector_rates")
 
 SOURCES = ["capi.cpp", "paged_plan.cpp", "flash_fwd.hip", "paged_fwd.hip", "kv_append.hip", "rope.hip",
            "int8_gemm.hip"]
@@ -66,6 +67,9 @@ def build(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB_PATH)
+    # the instruction-rate microbenchmark behind benchmarks/vector_rates.py (a
+    # stand-alone executable, not part of the library)
+    _run([HIPCC, *COMMON, "-x", "hip", os.path.join(PKG_DIR, "benchmarks", "vector_rates.hip"), "-o", RATES_PATH])
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH
