@@ -116,6 +116,30 @@ def test_layouts_scale_dtypes_and_shapes():
     assert int8_matmul_workspace_bytes(128, N, 4096) > 0  # split K
 
 
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_rows_layouts_bias_and_scale_dtypes(M, dtype):
+    """The row-streaming kernel of one or two activation rows: strided
+    activation rows (a column slice of a wider buffer, rows further apart
+    than K), a strided weight view, a bias, every scale dtype, a K tail past
+    the last 128-k step and N not a multiple of its 8 rows per workgroup --
+    bit for bit against the reference order in exact arithmetic."""
+    g = torch.Generator().manual_seed(20 + M)
+    K, N = 4160, 203
+    x = torch.randint(-3, 4, (M, K), generator=g).to(dtype)
+    w = torch.randint(-128, 128, (N, K), generator=g).to(torch.int8)
+    s = 2.0 ** -torch.randint(5, 8, (N,), generator=g).float()
+    bias = (torch.randint(-64, 64, (N,), generator=g).float() / 4).to(dtype)
+    want = int8_matmul_kernel_order_ref(x, w, s.to(dtype), bias)
+    wide = torch.zeros(M, K + 96, dtype=dtype)
+    wide[:, 48:48 + K] = x
+    wbig = torch.zeros(N, K + 64, dtype=torch.int8)
+    wbig[:, :K] = w
+    for sd in (torch.float16, torch.bfloat16, torch.float32):  # powers of two: exact in each
+        y = int8_matmul(wide.to(DEV)[:, 48:48 + K], wbig.to(DEV)[:, :K], s.to(sd).to(DEV), bias.to(DEV))
+        assert y.shape == (M, N) and torch.equal(y.cpu(), want), (M, dtype, sd)
+
+
 def test_int8_linear_close_to_float_layer():
     # tests/quant/test_int8_linear.py:9-21
     torch.manual_seed(0)
