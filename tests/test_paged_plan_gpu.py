@@ -47,6 +47,22 @@ def test_workloads_planned_equal_unplanned(name):
     assert_close(planned, ref, TOL[c.q.dtype], name)
 
 
+@pytest.mark.parametrize("B,Lq", [(3000, 1), (1200, 4)])
+def test_many_short_sequences_planned_equal_unplanned(B, Lq):
+    """Thousands of sequences of 1-40 tokens: a workgroup range then covers
+    many sequences, up to the per-range cap of sequences the launch geometry
+    keeps (more ranges than CUs when needed), most sequences end inside a
+    range and a few are split -- against the oracle, planned and unplanned
+    bit-identical."""
+    g = torch.Generator().manual_seed(B + Lq)
+    lens = (torch.randint(Lq, 41, (B,), generator=g)).tolist()
+    q, kp, vp, bt, lt = make_paged(lens, Lq, 64, torch.float16, 16, Hq=8, Hk=2, seed=B, vscale=0.5)
+    plain, planned, _ = _both(q, kp, vp, bt, lt)
+    assert torch.equal(planned, plain)
+    ref = paged_attention_ref(q, kp, vp, bt, lt, causal=True)
+    assert_close(planned, ref, TOL[torch.float16], f"B={B} Lq={Lq}")
+
+
 @pytest.mark.parametrize("Lq,bs,D,dtype", [(1, 16, 64, torch.float16), (5, 3, 128, torch.bfloat16),
                                            (3, 16, 16, torch.float16), (2, 7, 256, torch.bfloat16),
                                            (1, 1, 32, torch.float16)])
