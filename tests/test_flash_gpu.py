@@ -292,6 +292,24 @@ def test_workload_prefill_s2048():
     assert_close(out, ref, 2e-3, "prefill_s2048")
 
 
+@pytest.mark.parametrize("Lq,Lk", [(65536, 65536), (300, 65536)])
+def test_long_sequences_sampled_rows(Lq, Lk):
+    """64 K keys, fp16, head_dim 64, 8 / 2 heads, causal: a prefill of all of
+    them (the head-pair kernel, 4 * 16 * 512 items) and a 300-row chunk at
+    the end of the history (bottom-right mask: row i sees keys <= Lk - Lq +
+    i), checked on sampled rows against the oracle, with row and key
+    offsets past 2^16 and the element offsets of K / V past 2^22."""
+    g = torch.Generator().manual_seed(Lq)
+    q = (torch.randn(1, 8, Lq, 64, generator=g) / 8).half()
+    k = (torch.randn(1, 2, Lk, 64, generator=g) / 8).half()
+    v = torch.randn(1, 2, Lk, 64, generator=g).half()
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True).cpu()
+    assert not torch.isnan(out).any()
+    rows = sorted({0, 1, Lq // 2, Lq - 2, Lq - 1} | set(torch.randint(0, Lq, (11,), generator=g).tolist()))
+    ref = attention_rows_ref(q, k, v, rows, causal=True)
+    assert_close(out[:, :, rows], ref, 2e-3, f"Lq={Lq} Lk={Lk} sampled rows")
+
+
 def test_workload_prefill_s16384_sampled_rows():
     case = workloads.prefill_s16384()
     out = flash_attention(case.q.to(DEV), case.k.to(DEV), case.v.to(DEV), causal=True).cpu()
