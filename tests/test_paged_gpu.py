@@ -101,6 +101,42 @@ def test_long_contexts_split_and_max_context_hint():
     assert_close(b, ref, 1e-2, "split, max_context hint")
 
 
+def test_wide_pool_offsets():
+    """A pool view whose blocks lie 2^24 elements apart inside one larger
+    allocation (block stride >= 2^24, element offsets past 2^31 for block ids
+    >= 128): the launcher takes the 64-bit address path; the result equals
+    the oracle over the same blocks, planned and unplanned."""
+    from engine.attention import paged_plan
+
+    nb, bs, Hk, D, Lq = 136, 16, 2, 64, 3
+    lens = [1000, 700]
+    q, kp, vp, bt, ln = make_paged(lens, Lq, D, torch.float16, bs, Hq=8, Hk=Hk, seed=77,
+                                   extra=nb - sum(-(-c // bs) for c in lens), vscale=0.5)
+    assert kp.shape[0] == nb
+    # make sure the tables use blocks past 2^31 elements (ids >= 128)
+    used = set(bt[0, :-(-lens[0] // bs)].tolist()) | set(bt[1, :-(-lens[1] // bs)].tolist())
+    high = [i for i in range(128, nb) if i not in used]
+    if not any(i >= 128 for i in used):
+        bt[0, 0] = high[0]
+    stride = 1 << 24
+    views = []
+    for pool in (kp, vp):
+        big = torch.zeros(nb, stride, dtype=pool.dtype, device=DEV)
+        view = big[:, :bs * Hk * D].view(nb, bs, Hk, D)
+        view.copy_(pool.to(DEV))
+        assert view.stride(0) == stride
+        views.append(view)
+    ref = paged_attention_ref(q, kp, vp, bt, ln, causal=True)
+    args = (q.to(DEV), views[0], views[1], bt.to(DEV), ln.to(DEV))
+    out = paged_attention(*args, causal=True).cpu()
+    assert_close(out, ref, 2e-3, "wide offsets")
+    pl = paged_plan(ln, bt, Hq=8, Hk=Hk, Lq=Lq, D=D, num_blocks=nb, block_size=bs, max_context=max(lens), device=DEV)
+    planned = paged_attention(*args, causal=True, max_context=max(lens), plan=pl).cpu()
+    assert torch.equal(planned, out)
+    del views, args
+    torch.cuda.empty_cache()
+
+
 def test_context_beyond_hint_is_poisoned_not_truncated():
     lens = [3000, 100]
     q, kp, vp, bt, ln = make_paged(lens, 1, 64, torch.float16, 16, seed=22)
