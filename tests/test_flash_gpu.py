@@ -148,6 +148,34 @@ def test_strided_views_match_contiguous():
     assert torch.equal(out, out_c)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_huge_row_stride_uses_wide_copies(D):
+    """K and V rows 2^25 elements apart (views into one 2.7 GB allocation
+    each): a tile of rows spans more than 2^31 bytes, so the kernels form
+    64-bit per-lane addresses instead of 32-bit offsets from a tile base; the
+    result equals the oracle and the same data laid out contiguously, bit
+    for bit."""
+    g = torch.Generator().manual_seed(D)
+    H, Hk, L = 4, 2, 40
+    q = torch.randn(1, H, L, D, generator=g).half()
+    k = torch.randn(1, Hk, L, D, generator=g).half()
+    v = torch.randn(1, Hk, L, D, generator=g).half()
+    stride = 1 << 25
+    views = []
+    for t in (k, v):
+        big = torch.zeros(L, stride, dtype=t.dtype, device=DEV)
+        view = big[:, :Hk * D].view(L, Hk, D).permute(1, 0, 2).unsqueeze(0)
+        view.copy_(t.to(DEV))
+        assert view.stride(2) == stride
+        views.append(view)
+    out = flash_attention(q.to(DEV), views[0], views[1], causal=True).cpu()
+    dense = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True).cpu()
+    ref = flash_attention_ref(q.float(), k.float(), v.float(), causal=True)
+    assert_close(out, ref, 2e-3, f"D={D} huge row stride")
+    assert torch.equal(out, dense)
+    del views
+    torch.cuda.empty_cache()
+
 @pytest.mark.parametrize("D,B,Lq,Lk", [(64, 2, 100, 140), (64, 2, 300, 340), (64, 64, 300, 340), (64, 32, 1024, 1024),
                                       (128, 2, 100, 140)])
 def test_gqa_equals_expanded_mha_bitwise(D, B, Lq, Lk):
