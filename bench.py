@@ -16,7 +16,9 @@ The same line carries
   extra         the other workloads: paged decode (B=32, fp16) and speculative
                 verify (B=8, Lq=5, bf16) in GB/s against the 8 TB/s HBM peak,
                 timed while rotating over >= 512 MiB of KV pool copies so the
-                256 MiB Infinity Cache cannot hold them; the paged KV append
+                256 MiB Infinity Cache cannot hold them (back-to-back
+                launches; the planned calls also captured in a HIP graph and
+                replayed, as an engine step runs them); the paged KV append
                 of a prefill (4 x 2048 tokens) and of a decode step (32 x 1
                 token) in GB/s of bytes read + written; RoPE of the
                 prefill's q (4 x 32 x 2048 x 64) in GB/s; one layer's
@@ -672,6 +674,9 @@ def main():
             pl = PagedLaunch(c, dev, planned=True)
             ms = event_time_ms(pl, 40 * pl.copies, 2 * pl.copies)
             gbs = c.bytes / (ms / 1e3) / 1e9
+            # the same planned calls captured in a HIP graph (as an engine's decode step runs them)
+            ms_graph = graph_time_ms(pl, n_inner=max(20, pl.copies))
+            gbs_graph = c.bytes / (ms_graph / 1e3) / 1e9
             split = pl.plan.split
             del pl
             pd = PagedLaunch(c, dev)
@@ -679,6 +684,8 @@ def main():
             gbs_dev = c.bytes / (ms_dev / 1e3) / 1e9
             extra[name] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "us": round(ms * 1e3, 2),
                            "schedule": "host plan", "split_sequences": split,
+                           "graph_replay": {"GB/s": round(gbs_graph, 1), "frac_hbm": round(gbs_graph / PEAK_HBM_GBS, 4),
+                                            "us": round(ms_graph * 1e3, 2)},
                            "device_schedule": {"GB/s": round(gbs_dev, 1), "frac_hbm": round(gbs_dev / PEAK_HBM_GBS, 4),
                                                "us": round(ms_dev * 1e3, 2)},
                            "bytes": int(c.bytes), "pool_copies": pd.copies,

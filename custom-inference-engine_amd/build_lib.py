@@ -21,7 +21,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libcie_attn.so")
-RATES_PATH = os.path.join(BUILD, "vector_rates")
+# stand-alone microbenchmarks (benchmarks/<name>.hip -> _build/<name>), not part of the library
+BENCH_TOOLS = ("vector_rates", "read_floor")
 
 SOURCES = ["capi.cpp", "paged_plan.cpp", "flash_fwd.hip", "paged_fwd.hip", "kv_append.hip", "rope.hip",
            "int8_gemm.hip"]
@@ -67,9 +68,11 @@ def build(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB_PATH)
-    # the instruction-rate microbenchmark behind benchmarks/vector_rates.py (a
-    # stand-alone executable, not part of the library)
-    _run([HIPCC, *COMMON, "-x", "hip", os.path.join(PKG_DIR, "benchmarks", "vector_rates.hip"), "-o", RATES_PATH])
+    # the microbenchmarks behind benchmarks/vector_rates.py and read_floor.py
+    tools = [[HIPCC, *COMMON, "-x", "hip", os.path.join(PKG_DIR, "benchmarks", t + ".hip"), "-o", os.path.join(BUILD, t)]
+             for t in BENCH_TOOLS]
+    with ThreadPoolExecutor(max_workers=len(tools)) as ex:
+        list(ex.map(_run, tools))
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH
