@@ -22,7 +22,7 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libcie_attn.so")
 # stand-alone microbenchmarks (benchmarks/<name>.hip -> _build/<name>), not part of the library
-BENCH_TOOLS = ("vector_rates", "read_floor")
+BENCH_TOOLS = ("vector_rates", "read_floor", "prefill_step")
 
 SOURCES = ["capi.cpp", "paged_plan.cpp", "flash_fwd.hip", "paged_fwd.hip", "kv_append.hip", "rope.hip",
            "int8_gemm.hip"]
@@ -68,7 +68,7 @@ def build(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB_PATH)
-    # the microbenchmarks behind benchmarks/vector_rates.py and read_floor.py
+    # the microbenchmarks behind benchmarks/vector_rates.py, read_floor.py and prefill_step.py
     tools = [[HIPCC, *COMMON, "-x", "hip", os.path.join(PKG_DIR, "benchmarks", t + ".hip"), "-o", os.path.join(BUILD, t)]
              for t in BENCH_TOOLS]
     with ThreadPoolExecutor(max_workers=len(tools)) as ex:
