@@ -95,14 +95,32 @@ __device__ __forceinline__ int div_small(uint64_t n, uint32_t d) {
 // The plan header names the launch it was built for: every argument its
 // layout, ranges and validated block ids depend on, and the split count the
 // caller passes with it. Anything else of the plan is read only after this
-// check (one scalar load of the 16 header ints).
+// check. The 16 header ints are loaded together and compared without
+// short-circuit branches: one memory round trip, where a chain of compare-
+// and-branch steps waits for each field's load in turn.
 template <int D>
 __device__ __forceinline__ bool plan_matches(const PagedParams& p) {
-  const int32_t* P = p.plan;
-  return P[kPlMagic] == kPlanMagic && P[kPlWg] == p.Wg && P[kPlB] == p.B && P[kPlAppend] == (p.kn ? 1 : 0) &&
-         P[kPlSplit] == p.plan_split && P[kPlNG] == p.NG && P[kPlLq] == p.Lq && P[kPlD] == D &&
-         P[kPlNumBlocks] == p.num_blocks && P[kPlBlockSize] == p.block_size && P[kPlMaxBlocks] == p.max_blocks &&
-         P[kPlCtxLimit] == p.ctx_limit && P[kPlHq] == p.Hq;
+  const int4* P4 = reinterpret_cast<const int4*>(p.plan);  // the plan is 16-byte aligned
+  int32_t h[kPlanHeader];
+#pragma unroll
+  for (int i = 0; i < kPlanHeader / 4; ++i) {
+    const int4 v = P4[i];
+    h[4 * i] = v.x, h[4 * i + 1] = v.y, h[4 * i + 2] = v.z, h[4 * i + 3] = v.w;
+  }
+  bool ok = h[kPlMagic] == kPlanMagic;
+  ok &= h[kPlWg] == p.Wg;
+  ok &= h[kPlB] == p.B;
+  ok &= h[kPlAppend] == (p.kn ? 1 : 0);
+  ok &= h[kPlSplit] == p.plan_split;
+  ok &= h[kPlNG] == p.NG;
+  ok &= h[kPlLq] == p.Lq;
+  ok &= h[kPlD] == D;
+  ok &= h[kPlNumBlocks] == p.num_blocks;
+  ok &= h[kPlBlockSize] == p.block_size;
+  ok &= h[kPlMaxBlocks] == p.max_blocks;
+  ok &= h[kPlCtxLimit] == p.ctx_limit;
+  ok &= h[kPlHq] == p.Hq;
+  return ok;
 }
 
 __device__ __forceinline__ bool ctx_valid(const PagedParams& p, int ctx) {
