@@ -10,7 +10,9 @@ algorithmic work (4 B Hq D S(S+1)/2 FLOP per step). A step is one
 The same line carries
   roofline      the prefill kernel's achieved TFLOP/s (algorithmic FLOP per
                 launch / average launch duration from HIP events on the launch
-                stream) against the dense fp16 MFMA peak;
+                stream) against the dense fp16 MFMA peak, and against that
+                peak at the GFX clock the kernel holds under back-to-back
+                launches (amdsmi; null where it is not available);
   cpu_baseline  the fp32 oracle (the reference's naive algorithm) timed on the
                 host cores on the same workload;
   extra         the other workloads: paged decode (B=32, fp16) and speculative
@@ -474,6 +476,54 @@ def graph_time_ms(fn, n_inner=20, reps=20):
 
 
 SETTLE_S = 0.3  # seconds of untimed back-to-back work before a measurement
+PEAK_CLOCK_GHZ = 2.4  # the clock the spec peak assumes
+
+
+def gfx_clock_ghz(fn, seconds=0.8, skip=0.3):
+    """Median GFX clock (GHz) while fn runs back to back for `seconds`, from
+    the GPU metrics table (amdsmi, ~20 samples per second; the first `skip`
+    seconds dropped while the clock settles). None when amdsmi is not
+    available. The clock a kernel holds under load sets what fraction of the
+    spec peak (which assumes 2.4 GHz) it can reach."""
+    import threading
+
+    import torch
+
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+        handle = amdsmi.amdsmi_get_processor_handles()[0]
+    except Exception:  # noqa: BLE001 (no amdsmi, or no device it can open)
+        return None
+    samples = []
+    stop = threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            try:
+                v = amdsmi.amdsmi_get_gpu_metrics_info(handle).get("current_gfxclk")
+            except Exception:  # noqa: BLE001
+                v = None
+            if isinstance(v, list):  # per-XCD values
+                v = max((x for x in v if isinstance(x, int) and x not in (0xFFFF, 0xFFFFFFFF)), default=None)
+            if isinstance(v, int) and v not in (0xFFFF, 0xFFFFFFFF):
+                samples.append((time.perf_counter(), v))
+            time.sleep(0.05)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    sel = sorted(v for t, v in samples if t - t0 >= skip)
+    return sel[len(sel) // 2] / 1000.0 if sel else None
 
 
 def settle(fn, seconds=SETTLE_S):
@@ -663,6 +713,11 @@ def main():
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": traffic_from_summary(),
             "kernel": roof_name, "kernel_us": round(kern_ms * 1e3, 2)}
+    # the clock the kernel holds under back-to-back load, and the fraction of
+    # the peak at that clock (the spec peak assumes 2.4 GHz)
+    ghz = gfx_clock_ghz(fl)
+    roof["clock_ghz"] = ghz
+    roof["frac_at_clock"] = round(achieved / (PEAK_MFMA_F16_TFLOPS * ghz / PEAK_CLOCK_GHZ), 4) if ghz else None
 
     extra = {}
     if not args.no_extra:
@@ -721,8 +776,11 @@ def main():
         f5 = FlashLaunch(c5, dev)
         ms = event_time_ms(f5, 5, 1)
         t5 = c5.flops / (ms / 1e3) / 1e12
+        ghz5 = gfx_clock_ghz(f5, seconds=2.0, skip=0.5)
         extra["prefill_s16384"] = {"TFLOP/s": round(t5, 2), "frac_mfma": round(t5 / PEAK_MFMA_F16_TFLOPS, 4),
-                                   "us": round(ms * 1e3, 1), "dtype": "bf16"}
+                                   "us": round(ms * 1e3, 1), "dtype": "bf16", "clock_ghz": ghz5,
+                                   "frac_mfma_at_clock": round(t5 / (PEAK_MFMA_F16_TFLOPS * ghz5 / PEAK_CLOCK_GHZ), 4)
+                                   if ghz5 else None}
         del f5
         # the CPU-oracle case (fp32 on the host) run on the GPU with its tensors cast to fp16
         c1 = workloads.prefill_s128(dtype=torch.float16)
