@@ -1181,21 +1181,40 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
 
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
   // reference's softmax over an all -inf row; Lk == 0 gives zeros.
+  // O goes out through LDS so that every store instruction writes whole
+  // 128-byte rows: straight from the accumulators a store instruction would
+  // write 16 bytes into each of 32 rows. The ring is free once every wave
+  // is past its last tile; each wave stages its 64 (row, head) rows in its
+  // own quarter, 16-byte chunks XOR-swizzled by row pair, and reads back
+  // only what it wrote.
+  static_assert(4 * 2 * 32 * D <= C::NST * C::STAGE, "O staging fits the ring");
+  __syncthreads();  // no wave reads the ring any more
+  uint16_t* stg = ring + wave * (2 * 32 * D);
 #pragma unroll
   for (int rg = 0; rg < NRG; ++rg) {
     const float inv = p.Lk == 0 ? 0.f : 1.f / l[rg];
-    if (qi[rg] < p.Lq) {
-      uint16_t* orow = p.o + b * p.os0 + hq[rg] * p.os1 + (int64_t)qi[rg] * p.os2;
+    const int slot = 32 * rg + l32, sw = (slot >> 1) & 7;
 #pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
+    for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d = 32 * dt + 8 * g4 + 4 * hl;
-          const u32x2 w = {E::pack2(acc[rg][dt][4 * g4] * inv, acc[rg][dt][4 * g4 + 1] * inv),
-                           E::pack2(acc[rg][dt][4 * g4 + 2] * inv, acc[rg][dt][4 * g4 + 3] * inv)};
-          *reinterpret_cast<u32x2*>(orow + d) = w;
-        }
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int chunk = 4 * dt + g4;  // 16-byte chunk of d = 32 dt + 8 g4 .. +8
+        const u32x2 w = {E::pack2(acc[rg][dt][4 * g4] * inv, acc[rg][dt][4 * g4 + 1] * inv),
+                         E::pack2(acc[rg][dt][4 * g4 + 2] * inv, acc[rg][dt][4 * g4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(stg + slot * D + 8 * (chunk ^ sw) + 4 * hl) = w;
       }
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's staging writes are done
+  {
+    const int c = lane & 7;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int slot = 8 * i + (lane >> 3), rg = slot >> 5, r32 = slot & 31;
+      const int row = q0w + (HEADS ? 0 : 32 * rg) + r32;
+      const int head = HEADS ? kvh * G + 2 * g + rg : kvh * G + g;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + slot * D + 8 * (c ^ ((slot >> 1) & 7)));
+      if (row < p.Lq) *reinterpret_cast<u32x4*>(p.o + b * p.os0 + head * p.os1 + (int64_t)row * p.os2 + 8 * c) = v;
     }
   }
 }
