@@ -1,6 +1,7 @@
 """Builds libcie_attn.so (the gfx950 attention library) in-tree.
 
-    python custom-inference-engine_amd/build_lib.py
+    python custom-inference-engine_amd/build_lib.py              # the library
+    python custom-inference-engine_amd/build_lib.py --timeline   # its timeline build
 
 Every source is compiled for gfx950 with hipcc (objects under ``_build/``,
 compiled in parallel) and linked into ``custom-inference-engine_amd/libcie_attn.so``,
@@ -21,6 +22,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libcie_attn.so")
+TIMELINE_LIB_PATH = os.path.join(PKG_DIR, "libcie_attn_timeline.so")
 # stand-alone microbenchmarks (benchmarks/<name>.hip -> _build/<name>), not part of the library
 BENCH_TOOLS = ("vector_rates", "read_floor", "prefill_step")
 
@@ -53,21 +55,26 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(err + "\n")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source and link the shared library; returns its path."""
-    os.makedirs(BUILD, exist_ok=True)
+def _build_lib(out: str, objdir: str, defines: list[str]) -> None:
+    os.makedirs(objdir, exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
-        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmds.append([HIPCC, *COMMON, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *COMMON, *defines, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
         list(ex.map(_run, cmds))
-    tmp = LIB_PATH + ".tmp"
+    tmp = out + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source and link the shared library; returns its path."""
+    os.makedirs(BUILD, exist_ok=True)
+    _build_lib(LIB_PATH, BUILD, [])
     # the microbenchmarks behind benchmarks/vector_rates.py, read_floor.py and prefill_step.py
     tools = [[HIPCC, *COMMON, "-x", "hip", os.path.join(PKG_DIR, "benchmarks", t + ".hip"), "-o", os.path.join(BUILD, t)]
              for t in BENCH_TOOLS]
@@ -78,5 +85,18 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+def build_timeline(verbose: bool = False) -> str:
+    """The library once more with CIE_TIMELINE defined (per-workgroup stamps of
+    the head-pair prefill and paged kernels, read by benchmarks/timeline.py);
+    a measurement build, next to the product library, never loaded by it."""
+    _build_lib(TIMELINE_LIB_PATH, os.path.join(BUILD, "timeline"), ["-DCIE_TIMELINE"])
+    if verbose:
+        print(f"built {TIMELINE_LIB_PATH}")
+    return TIMELINE_LIB_PATH
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--timeline" in sys.argv[1:]:
+        build_timeline(verbose=True)
+    else:
+        build(verbose=True)

@@ -292,4 +292,41 @@ __device__ __forceinline__ u32x2 col4_odd(uint32_t a, uint32_t b, uint32_t c, ui
   return u32x2{(a >> 16) | (b & 0xffff0000u), (c >> 16) | (d & 0xffff0000u)};
 }
 
+// Per-workgroup timeline stamps for benchmarks/timeline.py, which builds the
+// library a second time with CIE_TIMELINE defined: thread 0 of each of the
+// first kTimelineMaxWg workgroups writes kTimelineSlots values of its own
+// (s_memrealtime, 100 MHz ticks, or a plain value) into a per-kernel device
+// array that an extern "C" accessor of the timeline build copies out. In
+// the product build every stamp compiles to nothing.
+#ifdef CIE_TIMELINE
+constexpr int kTimelineSlots = 8;
+constexpr int kTimelineMaxWg = 16384;
+#define CIE_STAMP(buf, slot)                                                                       \
+  do {                                                                                             \
+    if (threadIdx.x == 0 && blockIdx.x < (unsigned)kTimelineMaxWg)                                 \
+      (buf)[(size_t)blockIdx.x * kTimelineSlots + (slot)] = __builtin_amdgcn_s_memrealtime();      \
+  } while (0)
+#define CIE_STAMP_VALUE(buf, slot, v)                                                              \
+  do {                                                                                             \
+    if (threadIdx.x == 0 && blockIdx.x < (unsigned)kTimelineMaxWg)                                 \
+      (buf)[(size_t)blockIdx.x * kTimelineSlots + (slot)] = (unsigned long long)(v);               \
+  } while (0)
+// where the workgroup runs: XCC_ID in the high word, HW_ID (wave, SIMD, CU,
+// shader array, shader engine) in the low word
+#define CIE_STAMP_WHERE(buf, slot)                                                                 \
+  CIE_STAMP_VALUE(buf, slot,                                                                       \
+                  ((unsigned long long)__builtin_amdgcn_s_getreg((20) | ((4 - 1) << 11)) << 32) |  \
+                      __builtin_amdgcn_s_getreg((4) | ((32 - 1) << 11)))
+#else
+#define CIE_STAMP(buf, slot) \
+  do {                       \
+  } while (0)
+#define CIE_STAMP_VALUE(buf, slot, v) \
+  do {                                \
+  } while (0)
+#define CIE_STAMP_WHERE(buf, slot) \
+  do {                             \
+  } while (0)
+#endif
+
 }  // namespace cie

@@ -56,6 +56,10 @@
 
 namespace cie {
 
+#ifdef CIE_TIMELINE
+__device__ unsigned long long flash_timeline[kTimelineMaxWg * kTimelineSlots];  // benchmarks/timeline.py
+#endif
+
 // Every lambda of the kernel is inlined: the score arrays they take by
 // pointer must stay in registers.
 #define CIE_INLINE __attribute__((always_inline))
@@ -829,6 +833,8 @@ struct R64Cfg {
 
 template <int DTYPE, int D, bool HEADS>
 __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams p) {
+  CIE_STAMP(flash_timeline, 0);  // entry
+  CIE_STAMP_WHERE(flash_timeline, 5);
   using C = R64Cfg<D, HEADS>;
   using E = Elt<DTYPE>;
   constexpr int BN = C::BN, NRG = C::NRG;
@@ -1046,6 +1052,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
   const u32x2 sum_ones = {E::pack2(1.f, 1.f), E::pack2(1.f, 1.f)};
 
   vm_wait<0>();  // q (and RoPE tables) in registers before the copies start
+  CIE_STAMP(flash_timeline, 6);  // q in registers
   const int pro = min(C::NST - 1, n_tiles);
   for (int t = 0; t < pro; ++t) issue(t);
 
@@ -1053,6 +1060,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
   if (n_tiles > 0) {
     wait_tiles<C::PER_TILE, 2>(pro - 1);
     __syncthreads();
+    CIE_STAMP(flash_timeline, 7);  // first K/V tile in LDS
     qk(ring, sc);
     mask(0, sc);
 #pragma unroll
@@ -1167,6 +1175,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
           for (int dt = 0; dt < C::DT; ++dt) acc[rg][dt] = E::mfma(va[dt][cc], pb[rg][cc], acc[rg][dt]);
     }
   };
+  CIE_STAMP(flash_timeline, 1);  // loop start
+  CIE_STAMP_VALUE(flash_timeline, 4, n_tiles);
   f32x16 sb[NRG];
   static_assert(C::NST % 2 == 0, "stage and score buffer repeat after NST steps");
   for (int t = 0; t < n_tiles; t += C::NST) {
@@ -1179,6 +1189,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
     });
   }
 
+  CIE_STAMP(flash_timeline, 2);  // loop end
   // Epilogue: rows with keys but none visible give 0 * inf = NaN like the
   // reference's softmax over an all -inf row; Lk == 0 gives zeros.
   // O goes out through LDS so that every store instruction writes whole
@@ -1217,6 +1228,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams
       if (row < p.Lq) *reinterpret_cast<u32x4*>(p.o + b * p.os0 + head * p.os1 + (int64_t)row * p.os2 + 8 * c) = v;
     }
   }
+  CIE_STAMP(flash_timeline, 3);  // stores issued
 }
 
 // head_dim 128 runs the interleaved kernel (S=16384 bf16 causal: 1863 ->
@@ -1305,3 +1317,10 @@ hipError_t launch_flash(const FlashParams& p, int dtype, int D, hipStream_t stre
 }
 
 }  // namespace cie
+
+#ifdef CIE_TIMELINE
+// timeline build only: the stamps of the last flash_fwd_r64_kernel launch
+extern "C" int cie_timeline_flash(void* host, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(cie::flash_timeline), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif

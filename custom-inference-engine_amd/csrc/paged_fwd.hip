@@ -50,6 +50,10 @@
 
 namespace cie {
 
+#ifdef CIE_TIMELINE
+__device__ unsigned long long paged_timeline[kTimelineMaxWg * kTimelineSlots];  // benchmarks/timeline.py
+#endif
+
 constexpr float kLazyRescalePaged = 8.0f;
 
 // Lambdas of the kernel are inlined: the arrays they touch stay in registers.
@@ -180,6 +184,8 @@ __device__ __forceinline__ void store_row(uint16_t* row, const f32x16* acc, floa
 // the plain kernel carries none of its registers or branches.
 template <int DTYPE, int D, bool APPEND>
 __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(const PagedParams p) {
+  CIE_STAMP(paged_timeline, 0);  // entry
+  CIE_STAMP_WHERE(paged_timeline, 5);
   using C = PagedCfg<D>;
   using E = Elt<DTYPE>;
   extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
@@ -346,6 +352,9 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
   }
   }  // device-derived schedule
   __syncthreads();
+  CIE_STAMP(paged_timeline, 1);  // schedule in LDS
+  CIE_STAMP_VALUE(paged_timeline, 6, T);
+  CIE_STAMP_VALUE(paged_timeline, 7, ne);
   if (T == 0) return;
 
   // ---- per-lane constants -------------------------------------------------
@@ -550,6 +559,7 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
       wait_tiles_ahead<C::DPW>(min(NST - 1, T - 1 - n));
     }
     __syncthreads();  // tile n is in LDS for every wave
+    if (n == 0) CIE_STAMP(paged_timeline, 2);  // first tile in LDS
 
     if (n > 0 && n == c_end) begin_piece(n, std::false_type{});
 
@@ -666,6 +676,8 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
     __syncthreads();  // every wave is done with this stage before it is refilled
   }
 
+  CIE_STAMP(paged_timeline, 3);  // tile loop done
+
   // Fused append: the new tokens inside this range go into the pool, the
   // head group's rows of each (16-byte chunks over the whole workgroup).
   // Nothing in this launch reads those pool rows (the tiles holding them
@@ -712,6 +724,7 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
     }
   }
 
+  CIE_STAMP(paged_timeline, 4);  // end
 }
 
 // Second pass: combines the pieces of every split sequence. Eight lanes
@@ -984,3 +997,10 @@ hipError_t paged_scratch_ptr(void** ptr) {
 }
 
 }  // namespace cie
+
+#ifdef CIE_TIMELINE
+// timeline build only: the stamps of the last paged_fwd_kernel launch
+extern "C" int cie_timeline_paged(void* host, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(cie::paged_timeline), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
