@@ -261,6 +261,35 @@ __device__ __forceinline__ void vm_wait() {
 
 __device__ __forceinline__ void lgkm_wait0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Bring every 64-byte line of a kernel's argument block (BYTES of it, at
+// most 512) into the scalar cache with one batch of scalar loads and one
+// wait. The compiler loads the arguments where each branch first needs them:
+// the paged kernel made three dependent argument round trips before its
+// first memory request, each a scalar-cache miss on a CU's first wave. The
+// loaded dwords are discarded; touches at most 64 bytes apart, the last at
+// BYTES - 4, reach every line whatever the block's alignment.
+template <int BYTES>
+__device__ __forceinline__ void warm_kernargs() {
+  static_assert(BYTES >= 4 && BYTES <= 512 && BYTES % 4 == 0, "argument block size");
+  constexpr int L = BYTES - 4;
+  const auto ka = __builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t d;  // every load writes it; only the wait below orders them
+  asm volatile(
+      "s_load_dword %0, %1, %2\n\t"
+      "s_load_dword %0, %1, %3\n\t"
+      "s_load_dword %0, %1, %4\n\t"
+      "s_load_dword %0, %1, %5\n\t"
+      "s_load_dword %0, %1, %6\n\t"
+      "s_load_dword %0, %1, %7\n\t"
+      "s_load_dword %0, %1, %8\n\t"
+      "s_load_dword %0, %1, %9\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(d)
+      : "s"(ka), "n"(0), "n"(64 < L ? 64 : L), "n"(128 < L ? 128 : L), "n"(192 < L ? 192 : L),
+        "n"(256 < L ? 256 : L), "n"(320 < L ? 320 : L), "n"(384 < L ? 384 : L), "n"(448 < L ? 448 : L)
+      : "memory");
+}
+
 // XOR swizzle of the 16-byte chunks of row r in an LDS tile with S chunks per
 // row. LDS is 64 banks x 4 bytes (256-byte bank rows), so a row of S chunks
 // covers S/16 of a bank row and rows r, r + 16/S, ... share bank columns. Two

@@ -835,6 +835,7 @@ template <int DTYPE, int D, bool HEADS>
 __global__ __launch_bounds__(256, 2) void flash_fwd_r64_kernel(const FlashParams p) {
   CIE_STAMP(flash_timeline, 0);  // entry
   CIE_STAMP_WHERE(flash_timeline, 5);
+  warm_kernargs<sizeof(FlashParams)>();
   using C = R64Cfg<D, HEADS>;
   using E = Elt<DTYPE>;
   constexpr int BN = C::BN, NRG = C::NRG;

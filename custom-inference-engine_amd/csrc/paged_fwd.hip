@@ -186,6 +186,7 @@ template <int DTYPE, int D, bool APPEND>
 __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(const PagedParams p) {
   CIE_STAMP(paged_timeline, 0);  // entry
   CIE_STAMP_WHERE(paged_timeline, 5);
+  warm_kernargs<sizeof(PagedParams)>();
   using C = PagedCfg<D>;
   using E = Elt<DTYPE>;
   extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
@@ -786,6 +787,7 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const PagedParams p) {
   using E = Elt<DTYPE>;
   constexpr int Q4 = D / 4;
   static_assert(kMergeLanes == 8, "the butterfly below covers eight lanes");
+  warm_kernargs<sizeof(PagedParams)>();
   // thread index < 2^31 (paged_geometry bounds the merge grid): 32-bit
   // decomposition, invariant divisors by multiply-shift. With the plan's
   // merge table, workgroup (XCD x, slot s) takes part s % wpu of the x-th
