@@ -171,7 +171,8 @@ class PagedLaunch:
             self.plan = paged_plan(case.context_lens, case.block_tables, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb,
                                    block_size=bs, max_context=mc, device=dev)
             self._none3 = (ctypes.c_int64 * 3)(0, 0, 1)
-            self.tail = (None, None, self.plan.data.data_ptr(), self.plan.split, self.o.data_ptr(),
+            self.tail = (None, None, self.plan.data.data_ptr(), self.plan.data.numel() * 4, self.plan.split,
+                         self.o.data_ptr(),
                          self.ws.data_ptr(), ws, self._keep[0], self._none3, self._none3, *self._keep[1:],
                          B, Hq, Hk, Lq, D, nb, bs, mb, mc, ctypes.c_float(1.0 / math.sqrt(D)), 1,
                          _lib.DTYPE_CODES[self.q.dtype], None, None, 0, 0)

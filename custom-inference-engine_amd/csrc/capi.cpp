@@ -308,7 +308,7 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
                       void* stream, cie::RopeTables rope,
                       const void* k_new = nullptr, const void* v_new = nullptr,
                       const int64_t* kn_stride = nullptr, const int64_t* vn_stride = nullptr,
-                      const void* plan = nullptr, int plan_split = -1) {
+                      const void* plan = nullptr, size_t plan_bytes = 0, int plan_split = -1) {
   CIE_TRY(common_checks(Hq, Hk, D, dtype));
   if (B < 0 || Lq < 0) return fail(CIE_EINVAL, "negative size (B=%d, Lq=%d)", B, Lq);
   if (block_size < 1) return fail(CIE_EINVAL, "block_size must be positive, got %d", block_size);
@@ -371,6 +371,12 @@ static int paged_impl(const void* q, const void* k_cache, const void* v_cache,
   p.lens = context_lens;
   if (plan) {
     const cie::PlanLayout L = cie::paged_plan_layout(g, B, max_blocks_per_seq);
+    // the main pass reads a workgroup's range row in the same round trip as
+    // the header, before the header is checked: every offset of this
+    // launch's layout must lie in the buffer
+    if (plan_bytes < L.ints * sizeof(int32_t))
+      return fail(CIE_EINVAL, "plan: %zu bytes given, a plan for these arguments has %zu", plan_bytes,
+                  L.ints * sizeof(int32_t));
     p.plan = static_cast<const int32_t*>(plan);
     p.plan_ranges = (int)L.ranges;
     p.plan_entries = (int)L.entries;
@@ -451,7 +457,8 @@ int cie_paged_fwd(const void* q, const void* k_cache, const void* v_cache,
 }
 
 int cie_paged_fwd_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
-                     const int32_t* block_tables, const int32_t* context_lens, const void* plan, int plan_split,
+                     const int32_t* block_tables, const int32_t* context_lens, const void* plan,
+                     size_t plan_bytes, int plan_split,
                      void* o, void* workspace, size_t workspace_bytes,
                      const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
                      const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,
@@ -469,7 +476,7 @@ int cie_paged_fwd_ex(const void* q, const void* k_new, const void* v_new, void* 
   return paged_impl(q, k_cache, v_cache, block_tables, context_lens, o, workspace, workspace_bytes, q_stride,
                     kc_stride, vc_stride, o_stride, B, Hq, Hk, Lq, D, num_blocks, block_size, max_blocks_per_seq,
                     max_context, scale, causal, dtype, stream, rope, k_new, v_new, kn_stride, vn_stride, plan,
-                    plan ? plan_split : -1);
+                    plan_bytes, plan ? plan_split : -1);
 }
 
 int cie_paged_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,

@@ -31,6 +31,7 @@ constexpr int kAppendUnroll = 4;  // chunks per thread per trip, all loads in fl
 // (k_out), read by that attention too, is written normally.
 
 __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
+  warm_kernargs<sizeof(AppendParams)>();
   const int b = blockIdx.y;
   const int n0 = p.cu_new[b];
   const int L = p.cu_new[b + 1] - n0;
@@ -87,6 +88,7 @@ constexpr int kRopeUnroll = 2;
 
 template <int DTYPE>
 __global__ __launch_bounds__(256) void kv_append_rope_kernel(const AppendParams p) {
+  warm_kernargs<sizeof(AppendParams)>();
   const int b = blockIdx.y;
   const int n0 = p.cu_new[b];
   const int L = p.cu_new[b + 1] - n0;

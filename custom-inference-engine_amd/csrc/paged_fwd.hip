@@ -226,15 +226,21 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
   if (p.plan) {
     // ---- schedule from the host-built plan: this range's row, then its
     // entries and block ids (already validated) copied straight into LDS ----
+    // The range row is loaded beside the header, in the same round trip (the
+    // launch checked that the buffer holds every offset of its layout, so a
+    // row of a plan for other arguments is still inside it); it is used only
+    // when the header matches.
     const int32_t* P = p.plan;
+    const int32_t* row = P + p.plan_ranges + kPlanRangeInts * j;  // 16-byte aligned
+    const int4 r03 = *reinterpret_cast<const int4*>(row);        // first entry, entries, first id, ids
+    const int2 r45 = *reinterpret_cast<const int2*>(row + 4);    // S0, T
     const bool ok = plan_matches<D>(p);
-    const int32_t* row = P + p.plan_ranges + kPlanRangeInts * j;
-    if (ok) {
-      ne = min(row[1], kPagedEntries);
-      nid = min(row[3], kPagedIds);
-      S0 = row[4];
-      T = row[5];
-    }
+    // selects, not a branch: a branch would let the compiler sink the row's
+    // loads behind the header check
+    ne = ok ? min(r03.y, kPagedEntries) : 0;
+    nid = ok ? min(r03.w, kPagedIds) : 0;
+    S0 = ok ? r45.x : 0;
+    T = ok ? r45.y : 0;
     if (j == 0) {
       // sequences without tiles (zeros for an empty history, NaN for an
       // invalid length); every sequence NaN when the plan is not this launch's
@@ -248,11 +254,11 @@ __global__ __launch_bounds__(64 * paged_max_waves(D)) void paged_fwd_kernel(cons
       }
     }
     if (w == 0 && T > 0) {
-      const int32_t* es = P + p.plan_entries + 8 * row[0];
+      const int32_t* es = P + p.plan_entries + 8 * r03.x;
       const uint32_t ent_lds = lds_addr_of(ent);
       for (int x0 = 0; x0 < 8 * ne; x0 += 64)
         if (x0 + lane < 8 * ne) dma4(es + x0 + lane, ent_lds + 4u * (uint32_t)x0);
-      const int32_t* is = P + p.plan_ids + row[2];
+      const int32_t* is = P + p.plan_ids + r03.z;
       for (int x0 = 0; x0 < nid; x0 += 64)
         if (x0 + lane < nid) dma4(is + x0 + lane, sbt_lds + 4u * (uint32_t)x0);
       vm_wait<0>();

@@ -20,6 +20,7 @@ namespace cie {
 
 template <int DTYPE, int D, int HG>
 __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
+  warm_kernargs<sizeof(RopeParams)>();
   constexpr uint32_t UPR = D / 16;  // chunk pairs per row
   constexpr int HALF = D / 2;
   const uint32_t stride = gridDim.x * 256u;

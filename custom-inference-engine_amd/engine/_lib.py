@@ -91,7 +91,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.cie_paged_plan.argtypes = [_vp, ctypes.c_size_t, _vp, _vp, ctypes.c_int64, _i, _i, _i, _i, _i, _i, _i, _i,
                                    _i, _i]
     lib.cie_paged_plan.restype = _i
-    lib.cie_paged_fwd_ex.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, ctypes.c_size_t,
+    lib.cie_paged_fwd_ex.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _i, _vp, _vp,
+                                     ctypes.c_size_t,
                                      _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
                                      _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _i, _i,
                                      _vp, _vp, _i, _i, _vp]

@@ -419,7 +419,8 @@ def paged_attention(
         rp = rope_args(rope, D, q.device) if rope is not None else (None, None, 0, 0)
         with torch.cuda.device(q.device):
             rc = lib.cie_paged_fwd_ex(q.data_ptr(), *kn, k_cache.data_ptr(), v_cache.data_ptr(), None, None,
-                                      plan.data.data_ptr(), plan.split, out.data_ptr(),
+                                      plan.data.data_ptr(), plan.data.numel() * plan.data.element_size(),
+                                      plan.split, out.data_ptr(),
                                       workspace.data_ptr() if plan.split else None, ws_have if plan.split else 0,
                                       _lib.strides(q), *kst, _lib.strides(k_cache), _lib.strides(v_cache),
                                       _lib.strides(out), *args[12:], *rp, stream)

@@ -182,20 +182,26 @@ int cie_paged_plan(void* plan, size_t plan_bytes, const int32_t* context_lens, c
  * One entry for every paged attention variant: cie_paged_fwd with, each
  * optional, the fused append (k_new, v_new non-NULL: cie_paged_fwd_append),
  * RoPE (rope_cos, rope_sin non-NULL: the _rope entries) and a device copy of
- * a plan from cie_paged_plan (plan non-NULL; plan_split = its return value;
- * block_tables and context_lens are then not read and may be NULL: the plan
- * holds the lengths and validated block ids it was built from, and a plan
- * built from older lengths or tables attends over those). The results equal
- * the corresponding entry's bit for bit. The workspace must hold
+ * a plan from cie_paged_plan (plan non-NULL; plan_bytes = the size of that
+ * device buffer; plan_split = cie_paged_plan's return value; block_tables
+ * and context_lens are then not read and may be NULL: the plan holds the
+ * lengths and validated block ids it was built from, and a plan built from
+ * older lengths or tables attends over those). The results equal the
+ * corresponding entry's bit for bit. The workspace must hold
  * cie_paged_workspace_bytes bytes; with a plan whose plan_split is 0 it may
- * be NULL. The plan's header records B, Hq, Lq, head_dim, the head grouping,
- * num_blocks, block_size, max_blocks_per_seq, the context bound, the fused
- * append flag, the device's workgroup count and its split count; a plan
- * whose header differs from this call's arguments (or from plan_split) is
- * read no further and every output row is NaN.
+ * be NULL. A plan_bytes below cie_paged_plan_bytes for this call's
+ * arguments is rejected with CIE_EINVAL (the launch reads each workgroup's
+ * share of the plan in the same round trip as the plan's header, so every
+ * offset it computes must lie inside the buffer). The plan's header records
+ * B, Hq, Lq, head_dim, the head grouping, num_blocks, block_size,
+ * max_blocks_per_seq, the context bound, the fused append flag, the
+ * device's workgroup count and its split count; a plan whose header differs
+ * from this call's arguments (or from plan_split) is used no further and
+ * every output row is NaN.
  */
 int cie_paged_fwd_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
-                     const int32_t* block_tables, const int32_t* context_lens, const void* plan, int plan_split,
+                     const int32_t* block_tables, const int32_t* context_lens, const void* plan,
+                     size_t plan_bytes, int plan_split,
                      void* o, void* workspace, size_t workspace_bytes,
                      const int64_t* q_stride, const int64_t* kn_stride, const int64_t* vn_stride,
                      const int64_t* kc_stride, const int64_t* vc_stride, const int64_t* o_stride,

@@ -118,7 +118,8 @@ def _launch_ex(lib, args, o, plan, split, *, Hq, Hk, Lq, D, nb, bs, mb, max_cont
     none3 = (ctypes.c_int64 * 3)(0, 0, 1)
     ws = torch.empty(16 << 20, dtype=torch.uint8, device=DEV)
     rc = lib.cie_paged_fwd_ex(args[0].data_ptr(), None, None, args[1].data_ptr(), args[2].data_ptr(), None, None,
-                              plan.data_ptr(), split, o.data_ptr(), ws.data_ptr(), ws.numel(),
+                              plan.data_ptr(), plan.numel() * plan.element_size(), split, o.data_ptr(),
+                              ws.data_ptr(), ws.numel(),
                               st[0], none3, none3, st[1], st[2], st[3], args[0].shape[0], Hq, Hk, Lq, D, nb, bs,
                               mb, max_context, ctypes.c_float(1.0 / math.sqrt(D)), 1, 0, None, None, 0, 0,
                               _lib.stream_handle(torch.device(DEV)))
@@ -171,10 +172,39 @@ def test_plan_for_other_arguments_gives_nan(field, over, dsplit):
                      D=over.get("D", D), num_blocks=nb + over.get("num_blocks_add", 0),
                      block_size=over.get("block_size", bs), max_context=over.get("max_context"),
                      for_append=over.get("for_append", False), device=DEV)
+    # a buffer smaller than this launch's plan is refused before any launch;
+    # padded to that size (zeros past the plan) it reaches the header check
+    need = lib.cie_paged_plan_bytes(q.shape[0], Hq, Hk, Lq, D, 0, bs, mb)
+    data = bad.data
+    if data.numel() * 4 < need:
+        o = torch.zeros_like(args[0])
+        with pytest.raises(ValueError, match="plan"):
+            _launch_ex(lib, args, o, data, bad.split + dsplit, Hq=Hq, Hk=Hk, Lq=Lq, D=D, nb=nb, bs=bs, mb=mb,
+                       max_context=0)
+        assert not o.any()
+        data = torch.zeros(need // 4, dtype=torch.int32, device=DEV)
+        data[:bad.data.numel()] = bad.data
     o = torch.zeros_like(args[0])
-    _launch_ex(lib, args, o, bad.data, bad.split + dsplit, Hq=Hq, Hk=Hk, Lq=Lq, D=D, nb=nb, bs=bs, mb=mb,
+    _launch_ex(lib, args, o, data, bad.split + dsplit, Hq=Hq, Hk=Hk, Lq=Lq, D=D, nb=nb, bs=bs, mb=mb,
                max_context=0)
     assert torch.isnan(o).all(), field
+
+
+def test_plan_buffer_smaller_than_the_launch_is_refused():
+    """plan_bytes below cie_paged_plan_bytes for the call's arguments:
+    CIE_EINVAL before any launch, the output untouched."""
+    Hq, Hk, Lq, D, bs = 8, 2, 1, 64, 16
+    q, kp, vp, bt, lt = make_paged([40, 300], Lq, D, torch.float16, bs, Hq=Hq, Hk=Hk, seed=5)
+    nb, mb = kp.shape[0], bt.shape[1]
+    args = [t.to(DEV) for t in (q, kp, vp, bt, lt)]
+    lib = _lib.load()
+    good = paged_plan(lt, bt, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb, block_size=bs, device=DEV)
+    assert good.data.numel() * 4 == lib.cie_paged_plan_bytes(2, Hq, Hk, Lq, D, 0, bs, mb)
+    o = torch.zeros_like(args[0])
+    with pytest.raises(ValueError, match="plan"):
+        _launch_ex(lib, args, o, good.data[:-1], good.split, Hq=Hq, Hk=Hk, Lq=Lq, D=D, nb=nb, bs=bs, mb=mb,
+                   max_context=0)
+    assert not o.any()
 
 
 def test_attention_section_with_step_plan_equals_without():
