@@ -282,6 +282,18 @@ def test_deterministic():
     assert torch.equal(flash_attention(q, k, v, causal=True), flash_attention(q, k, v, causal=True))
 
 
+def test_headline_workload_is_bit_identical_run_to_run():
+    """prefill_s2048 on the head-pair kernel, three more launches with another
+    launch between each: the same bits (every row's arithmetic is fixed; no
+    cross-workgroup reduction)."""
+    c = workloads.prefill_s2048(DEV)
+    assert prefill_kernel(4, 32, 8, 2048, 2048, 64, True, torch.float16) == "r64_heads"
+    first = flash_attention(c.q, c.k, c.v, causal=True)
+    for _ in range(3):
+        flash_attention(c.k.repeat_interleave(4, dim=1), c.k, c.v, causal=True)
+        assert torch.equal(flash_attention(c.q, c.k, c.v, causal=True), first)
+
+
 def test_explicit_scale():
     q, k, v = _inputs(1, 4, 2, 64, 64, 64, torch.float16, seed=11)
     out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=False, scale=0.05)

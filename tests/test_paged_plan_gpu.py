@@ -232,3 +232,26 @@ def test_attention_section_with_step_plan_equals_without():
             outs.append((attention_section(q, k, v, 0, cache, step).cpu(), cache.k[0].cpu(), cache.v[0].cpu()))
         for a, b in zip(outs[0], outs[1]):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("name", ["decode_b32", "verify_b8"])
+def test_workloads_are_bit_identical_run_to_run(name):
+    """The split sequences' pieces are fixed by the schedule and merged in
+    piece order by a fixed butterfly, so repeated launches (planned and
+    unplanned, into fresh outputs, with other launches between them) give
+    the same bits."""
+    from benchmarks import workloads
+
+    c = workloads.WORKLOADS[name]()
+    B, Hq, Lq, D = c.q.shape
+    nb, bs, Hk, _ = c.k_pool.shape
+    mc = int(c.context_lens.max())
+    args = [t.to(DEV) for t in (c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens)]
+    pl = paged_plan(c.context_lens, c.block_tables, Hq=Hq, Hk=Hk, Lq=Lq, D=D, num_blocks=nb, block_size=bs,
+                    max_context=mc, device=DEV)
+    first = paged_attention(*args, causal=True, plan=pl, max_context=mc)
+    for _ in range(3):
+        other = torch.randn(B, Hq, Lq, D, device=DEV).to(c.q.dtype)  # a different launch in between
+        paged_attention(other, *args[1:], causal=True, max_context=mc)
+        assert torch.equal(paged_attention(*args, causal=True, plan=pl, max_context=mc), first)
+        assert torch.equal(paged_attention(*args, causal=True, max_context=mc), first)
